@@ -1,0 +1,198 @@
+"""Benchmark of the tropical GEMM hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P]
+
+A step is one call of the C ABI entry point ``tg_gemm_ws`` on the config's
+synthetic inputs (already resident in HBM): for argmax configs that is the
+B^T staging kernel, the tiled GEMM kernel and the argmax resolve kernel.
+Steps are timed with HIP events on the stream the kernels run on (torch's
+current stream), bracketed by device synchronisation.  ``value`` is tropical
+GOP/s = 2*M*N*K / t_step, the reference's own "GFLOPS-equivalent" count
+(crates/tropical-gemm/examples/bench_rust.rs:121).
+
+The CPU baseline is the single-thread restatement of the reference's CPU
+argmax path (oracle/tg_oracle.c, ``tgo_portable_argmax_f32``) timed on a row
+slab of the same workload on this host.
+
+Prints one JSON line.  Only one GPU is supported: ``--gpus`` > 1 exits.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tropical-gemm_amd"))
+
+METRIC = ("tropical GOP/s (2·M·N·K) MaxPlus f32 4096³ +argmax, 1 GPU; "
+          "% VALU peak")
+PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector peak
+HBM_PEAK_GBS = 8000.0         # MI355X published HBM3E bandwidth
+# Tropical VALU ceiling for f32 without packed FP32 ops: one v_add_f32 per
+# (i,j,k) plus half a v_max3_f32 -> 1.5 issue slots for 2 ops; 256 CU x 64
+# lanes x 2.4 GHz = 39.32e12 slots/s  ->  52.4e12 ops/s.
+TROP_CEILING_TOPS = 39.32 * 2 / 1.5
+DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def run_cpu_baseline(rows: int) -> dict:
+    """Single-thread reference-algorithm restatement on a row slab of P."""
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0x7E0000)
+    k = n = 4096
+    a = rng.standard_normal((rows, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    t0 = time.perf_counter()
+    oracle.portable_argmax_f32("maxplus", a, b)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(2.0 * rows * n * k / dt / 1e9, 3),
+        "unit": "GOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{rows}x4096x4096 row slab of P (MaxPlus f32 +argmax), reference CPU argmax "
+                   f"algorithm (BLIS PORTABLE tiling, 4x4 scalar microkernel) restated in C, "
+                   f"1 thread, {dt:.1f} s on {cpu_model()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4"])
+    ap.add_argument("--cpu-rows", type=int, default=768,
+                    help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path.  Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import workloads
+    from tropical_gemm import _native as nat
+
+    if not torch.cuda.is_available():
+        print("no HIP device visible", file=sys.stderr)
+        return 1
+    lib = nat.load()
+    dev = torch.device("cuda", 0)
+    cfg = workloads.CONFIGS[args.config]
+    m, n, k = cfg["m"], cfg["n"], cfg["k"]
+    a, b = workloads.make_inputs(args.config, dev)
+    tdt = a.dtype
+    c = torch.empty((m, n), dtype=tdt, device=dev)
+    am = torch.empty((m, n), dtype=torch.int32, device=dev) if cfg["argmax"] else None
+    dt = nat.DTYPE[cfg["dtype"]]
+    ws_bytes = lib.tg_gemm_workspace_size(dt, 1, m, n, k, 1 if cfg["argmax"] else 0)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    s_ptr = ctypes.c_void_p(stream.cuda_stream)
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sr = nat.SEMIRING[cfg["semiring"]]
+
+    def step():
+        rc = lib.tg_gemm_ws(0, sr, dt, 0, p(a), p(b), p(c), p(am), m, n, k, p(ws), ws_bytes, s_ptr)
+        if rc != 0:
+            raise nat.HipError(rc, nat.last_error())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    # Post-timing sanity check (outside the timed region): every output equals
+    # the product at its argmax, bit-exactly.
+    check = None
+    if am is not None:
+        kk = am.long()
+        aw = torch.gather(a, 1, kk)
+        bw = torch.gather(b, 0, kk)
+        prod = aw * bw if cfg["semiring"] == "maxmul" else aw + bw
+        check = bool(torch.equal(prod, c))
+
+    ops = 2.0 * m * n * k
+    gops = ops / (ms_step / 1e3) / 1e9
+    achieved_tops = gops / 1e3
+    esize = a.element_size()
+    algo_bytes = esize * (m * k + k * n + m * n) + (4 * m * n if am is not None else 0)
+    out = {
+        "metric": METRIC,
+        "value": round(gops, 2),
+        "unit": "GOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAME[cfg["dtype"]],
+        "data": "synthetic (seeded torch Philox on device; workloads.py)",
+        "config": {"workload": {"P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
+                                "C1": "C1: MaxPlus f32 1024^3 +argmax",
+                                "C2": "C2: MinPlus f32 4096^3 +argmax, 10% +inf, zero diagonal",
+                                "C3": "C3: MaxMul f32 8192x2048x4096 value-only",
+                                "C4": "C4: MaxPlus i32 262144x128x128 +argmax"}[args.config],
+                   "semiring": cfg["semiring"], "m": m, "n": n, "k": k,
+                   "argmax": cfg["argmax"], "layout": "row-major", "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "bound": "valu",
+            "achieved": round(achieved_tops, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved_tops / PEAK_FP32_TFLOPS, 4),
+            "traffic": None,
+            "ops_per_launch": ops,
+            "timed": "tg_gemm_ws step (B^T staging + tile GEMM + argmax resolve)",
+            "trop_valu_ceiling": round(TROP_CEILING_TOPS, 1),
+            "frac_of_trop_valu_ceiling": round(achieved_tops / TROP_CEILING_TOPS, 4),
+            "algorithmic_bytes": algo_bytes,
+            "algorithmic_GBps": round(algo_bytes / (ms_step / 1e3) / 1e9, 1),
+        },
+        "wall_s_timed_region": round(wall, 4),
+        "argmax_consistency_check": check,
+        "device": torch.cuda.get_device_name(dev),
+    }
+    if args.cpu_rows > 0 and args.config == "P":
+        out["cpu_baseline"] = run_cpu_baseline(args.cpu_rows)
+        out["gpu_vs_cpu_baseline"] = round(gops / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,114 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tropical_gemm import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tropical_gemm_hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_built():
+    assert os.path.exists(nat.library_path()), "run __graft_entry__.build() first"
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = nat.load()
+    declared = header_symbols()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+    assert sorted(nat.SIGNATURES) == declared, "ctypes signatures out of sync with the header"
+
+
+def test_version_and_status_strings():
+    lib = nat.load()
+    assert lib.tg_version() == 1
+    assert lib.tg_status_string(nat.TG_ERR_DIMENSION_MISMATCH) == b"dimension mismatch"
+    assert lib.tg_status_string(999) == b"unknown status"
+
+
+def _gemm(**kw):
+    args = dict(device=0, sr=0, dt=0, layout=0, A=1, B=1, C=1, argmax=None, m=4, n=4, k=4)
+    args.update(kw)
+    lib = nat.load()
+    p = lambda v: None if v is None else ctypes.c_void_p(v)  # noqa: E731
+    return lib.tg_gemm(args["device"], args["sr"], args["dt"], args["layout"], p(args["A"]),
+                       p(args["B"]), p(args["C"]), p(args["argmax"]), args["m"], args["n"],
+                       args["k"], None)
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(sr=7), nat.TG_ERR_INVALID_ARGUMENT, "unknown semiring"),
+    (dict(dt=9), nat.TG_ERR_INVALID_ARGUMENT, "unknown dtype"),
+    (dict(layout=3), nat.TG_ERR_INVALID_ARGUMENT, "unknown layout"),
+    (dict(m=-1), nat.TG_ERR_DIMENSION_MISMATCH, "negative dimension"),
+    (dict(k=2**31), nat.TG_ERR_DIMENSION_MISMATCH, "2^31-1"),
+    (dict(C=None), nat.TG_ERR_INVALID_ARGUMENT, "C is NULL"),
+    (dict(A=None), nat.TG_ERR_INVALID_ARGUMENT, "A or B is NULL"),
+])
+def test_gemm_argument_validation(kw, status, needle):
+    assert _gemm(**kw) == status
+    assert needle in nat.last_error()
+
+
+def test_workspace_size_and_validation():
+    lib = nat.load()
+    assert lib.tg_gemm_workspace_size(0, 1, 64, 64, 64, 0) == 0
+    need = lib.tg_gemm_workspace_size(0, 1, 100, 70, 33, 1)
+    assert need >= 70 * 33 * 4 and need % 256 == 0
+    assert lib.tg_gemm_workspace_size(1, 2, 10, 10, 10, 1) >= 2 * 10 * 10 * 8
+    rc = lib.tg_gemm_ws(0, 0, 0, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                        ctypes.c_void_p(16), 8, 8, 8, ctypes.c_void_p(256), 16, None)
+    assert rc == nat.TG_ERR_INVALID_ARGUMENT and "workspace too small" in nat.last_error()
+
+
+def test_batched_output_overlap_rejected():
+    lib = nat.load()
+    p = ctypes.c_void_p(4096)
+    rc = lib.tg_gemm_strided_batched(0, 0, 0, 0, p, p, p, None, 3, 4, 4, 4, 16, 16, 8, None)
+    assert rc == nat.TG_ERR_DIMENSION_MISMATCH and "overlap" in nat.last_error()
+
+
+def test_backward_rejects_integer_dtype():
+    lib = nat.load()
+    p = ctypes.c_void_p(4096)
+    rc = lib.tg_backward_a(0, nat.DTYPE["i32"], 0, p, p, p, 4, 4, 4, None)
+    assert rc == nat.TG_ERR_UNSUPPORTED and "f32/f64" in nat.last_error()
+
+
+def test_maxmul_backward_needs_operand():
+    lib = nat.load()
+    p = ctypes.c_void_p(4096)
+    rc = lib.tg_maxmul_backward_a(0, 0, 0, p, p, None, p, 4, 4, 4, None)
+    assert rc == nat.TG_ERR_INVALID_ARGUMENT and "other operand" in nat.last_error()
+
+
+def test_hip_error_maps_reference_variants():
+    e = nat.HipError(nat.TG_ERR_DIMENSION_MISMATCH, "A.cols (3) != B.rows (4)")
+    assert e.kind == "DimensionMismatch" and "A.cols" in str(e)
+    assert nat.HipError(nat.TG_ERR_NO_DEVICE, "x").kind == "NoDevice"
+
+
+def test_python_layer_rejects_host_tensors():
+    torch = pytest.importorskip("torch")
+    from tropical_gemm import ops
+
+    a = torch.zeros(2, 3)
+    b = torch.zeros(3, 2)
+    with pytest.raises(ValueError, match="device tensors"):
+        ops.gemm("maxplus", a, b)
+    with pytest.raises(ValueError, match="Expected 2D"):
+        ops.gemm("maxplus", a, torch.zeros(3))
+    with pytest.raises(ValueError, match="same dtype"):
+        ops.gemm("maxplus", a, torch.zeros(3, 2, dtype=torch.float64))

@@ -1,0 +1,112 @@
+"""The benchmark configurations at their full sizes, checked against the oracle
+(bit-exact values and argmax) plus size-independent invariants:
+
+* argmax consistency: C[i,j] == A[i,k*] (x) B[k*,j] bit-exactly;
+* C2 shortest-path structure: zero diagonal gives C[i,i] == 0;
+* C5: sum(grad_A) == sum(grad_B) == sum(dC) (every gradient lands once).
+"""
+import numpy as np
+import pytest
+
+import workloads
+from oracle import oracle
+from tests import tg_cases as tc
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _run(name, with_argmax):
+    from tropical_gemm import ops
+
+    cfg = workloads.CONFIGS[name]
+    a, b = workloads.make_inputs(name, DEV)
+    print(f"[case] config {name} {cfg}", flush=True)
+    c, am = ops.gemm(cfg["semiring"], a, b, with_argmax)
+    torch.cuda.synchronize()
+    return cfg, a, b, c, am
+
+
+def _check_consistency(sr, a, b, c, am):
+    """C[i,j] == A[i,k*] (x) B[k*,j] on the GPU, bit-exact, without the oracle."""
+    k_idx = am.long()
+    a_w = torch.gather(a, 1, k_idx)
+    b_w = torch.gather(b, 0, k_idx)  # B[k*, j]: gather along dim 0 with index (m, n)
+    if sr == "maxmul":
+        prod = a_w * b_w
+    else:
+        prod = a_w + b_w
+    assert torch.equal(prod, c)
+
+
+@pytest.mark.parametrize("name", ["P", "C2"])
+def test_square_argmax_configs_full_size(name):
+    cfg, a, b, c, am = _run(name, True)
+    _check_consistency(cfg["semiring"], a, b, c, am)
+    c_ref, am_ref = oracle.gemm(cfg["semiring"], a.cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(tc.bits(c.cpu().numpy()), tc.bits(c_ref))
+    np.testing.assert_array_equal(am.cpu().numpy(), am_ref.astype(np.int32))
+    if name == "C2":
+        d = torch.diagonal(c)
+        assert torch.all(d == 0)
+
+
+def test_c1_value_only_and_argmax():
+    cfg, a, b, c, am = _run("C1", True)
+    c_ref, am_ref = oracle.gemm("maxplus", a.cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(tc.bits(c.cpu().numpy()), tc.bits(c_ref))
+    np.testing.assert_array_equal(am.cpu().numpy(), am_ref.astype(np.int32))
+    _, _, _, c2, _ = _run("C1", False)
+    np.testing.assert_array_equal(tc.bits(c2.cpu().numpy()), tc.bits(c_ref))
+
+
+def test_c3_maxmul_value_only_full_and_odd_shape():
+    cfg, a, b, c, _ = _run("C3", False)
+    c_ref, _ = oracle.gemm("maxmul", a.cpu().numpy(), b.cpu().numpy(), with_argmax=False)
+    np.testing.assert_array_equal(tc.bits(c.cpu().numpy()), tc.bits(c_ref))
+    assert torch.all(c > 0)
+    # Odd shape with the same distribution exercises every ragged tile edge.
+    from tropical_gemm import ops
+
+    a2, b2 = a[:8191, :2047].contiguous(), b[:2047, :4095].contiguous()
+    c2, _ = ops.gemm("maxmul", a2, b2, False)
+    c2_ref, _ = oracle.gemm("maxmul", a2.cpu().numpy(), b2.cpu().numpy(), with_argmax=False)
+    np.testing.assert_array_equal(tc.bits(c2.cpu().numpy()), tc.bits(c2_ref))
+
+
+def test_c4_viterbi_i32_full_size():
+    cfg, a, b, c, am = _run("C4", True)
+    _check_consistency("maxplus", a, b, c, am)
+    c_ref, am_ref = oracle.gemm("maxplus", a.cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(c.cpu().numpy(), c_ref)
+    np.testing.assert_array_equal(am.cpu().numpy(), am_ref.astype(np.int32))
+
+
+def test_c5_backward_full_size():
+    from tropical_gemm import ops
+
+    cfg, a, b, c, am = _run("C5", True)
+    g = workloads.make_grad("C5", 4096, 4096, DEV)
+    ga = ops.backward_a(g, am, 4096)
+    gb = ops.backward_b(g, am, 4096)
+    torch.cuda.synchronize()
+    gs = float(g.double().sum())
+    assert abs(float(ga.double().sum()) - gs) < 1e-2
+    assert abs(float(gb.double().sum()) - gs) < 1e-2
+    g_np = g.cpu().numpy()
+    am_np = am.cpu().numpy().astype(np.uint32)
+    ga_ref = oracle.backward_a(g_np, am_np, 4096)
+    gb_ref = oracle.backward_b(g_np, am_np, 4096)
+    # Per-element bound 4 * n * 2^-24 * sum|terms| (see test_gpu_backward.py).
+    for got, ref, which in ((ga.cpu().numpy(), ga_ref, "a"), (gb.cpu().numpy(), gb_ref, "b")):
+        m, n = g_np.shape
+        ii, jj = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+        idx = (ii, am_np.astype(np.int64)) if which == "a" else (am_np.astype(np.int64), jj)
+        cnt = np.zeros(got.shape)
+        s = np.zeros(got.shape)
+        np.add.at(cnt, idx, 1)
+        np.add.at(s, idx, np.abs(g_np.astype(np.float64)))
+        diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        assert np.all(diff <= 4 * cnt * 2.0**-24 * s)

@@ -1,0 +1,292 @@
+"""GPU parity: every forward entry point of the C ABI against the oracle,
+bit-exact (values compared as bit patterns, argmax exactly)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests import tg_cases as tc
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TORCH_DT = {np.dtype(np.float32): torch.float32, np.dtype(np.float64): torch.float64,
+            np.dtype(np.int32): torch.int32, np.dtype(np.int64): torch.int64}
+DT_NAME = {np.dtype(np.float32): "f32", np.dtype(np.float64): "f64",
+           np.dtype(np.int32): "i32", np.dtype(np.int64): "i64"}
+
+
+def _nat():
+    from tropical_gemm import _native
+
+    return _native
+
+
+def _dev(x: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def gpu_gemm(sr, a, b, with_argmax=True, layout="row", api="alloc"):
+    """Run tg_gemm (api='alloc') or tg_gemm_ws (api='ws') through ctypes.
+    For layout='col' the numpy inputs are row-major logical matrices that are
+    handed over in column-major storage; results come back row-major."""
+    nat = _nat()
+    lib = nat.load()
+    m, k = a.shape
+    n = b.shape[1]
+    if layout == "col":
+        ta, tb = _dev(np.asfortranarray(a).T.copy()), _dev(np.asfortranarray(b).T.copy())
+    else:
+        ta, tb = _dev(a), _dev(b)
+    c = torch.empty(m * n, dtype=TORCH_DT[a.dtype], device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV) if with_argmax else None
+    dt = nat.DTYPE[DT_NAME[a.dtype]]
+    lay = nat.LAYOUT[layout]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if api == "alloc":
+        nat.check(lib.tg_gemm(0, nat.SEMIRING[sr], dt, lay, _p(ta), _p(tb), _p(c), _p(am), m, n, k,
+                              stream))
+    else:
+        ws_bytes = lib.tg_gemm_workspace_size(dt, 1, m, n, k, int(with_argmax))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+        nat.check(lib.tg_gemm_ws(0, nat.SEMIRING[sr], dt, lay, _p(ta), _p(tb), _p(c), _p(am), m,
+                                 n, k, _p(ws), ws_bytes, stream))
+    torch.cuda.synchronize()
+    if layout == "col":
+        c_np = c.cpu().numpy().reshape(n, m).T
+        am_np = am.cpu().numpy().reshape(n, m).T if with_argmax else None
+    else:
+        c_np = c.cpu().numpy().reshape(m, n)
+        am_np = am.cpu().numpy().reshape(m, n) if with_argmax else None
+    return c_np, am_np
+
+
+def assert_exact(c, am, c_ref, am_ref):
+    np.testing.assert_array_equal(tc.bits(c), tc.bits(c_ref))
+    if am is not None:
+        np.testing.assert_array_equal(am.astype(np.int64), am_ref.astype(np.int64))
+
+
+# ---------------------------------------------------------------------------
+# Golden fixtures through the C ABI (2-D via tg_gemm, 3-D via strided batched)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", tc.fixture_paths(), ids=lambda p: p.split("fixtures/")[-1])
+def test_golden_fixture_on_gpu(path):
+    from tropical_gemm import ops
+
+    fx = tc.load_fixture(path)
+    if fx["a"].ndim == 3:
+        c, am = ops.gemm_batched(fx["algebra"], _dev(fx["a"]), _dev(fx["b"]), True)
+    else:
+        c, am = ops.gemm(fx["algebra"], _dev(fx["a"]), _dev(fx["b"]), True)
+    assert_exact(c.cpu().numpy(), am.cpu().numpy(), fx["c"], fx["argmax"])
+
+
+@pytest.mark.parametrize("case", tc.HAND_CASES, ids=lambda c: c[5])
+def test_hand_cases_on_gpu(case):
+    sr, a, b, c_exp, am_exp, _ = case
+    for dtype in (np.float32, np.float64):
+        c, am = gpu_gemm(sr, a.astype(dtype), b.astype(dtype))
+        np.testing.assert_array_equal(c, np.array(c_exp, dtype=dtype))
+        np.testing.assert_array_equal(am, np.array(am_exp))
+
+
+# ---------------------------------------------------------------------------
+# Random shapes: every dtype x semiring x {value, argmax}, ragged edges
+# ---------------------------------------------------------------------------
+
+SHAPES = [(1, 1, 1), (1, 37, 1), (5, 3, 7), (64, 32, 64), (129, 65, 63), (130, 31, 200),
+          (257, 100, 129), (33, 1000, 17)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "i32", "i64"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_random_shapes_argmax(sr, dt):
+    rng = np.random.default_rng(100 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in SHAPES:
+        print(f"[case] argmax {sr} {dt} m={m} k={k} n={n}", flush=True)
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        c, am = gpu_gemm(sr, a, b, True)
+        c_ref, am_ref = oracle.gemm(sr, a, b)
+        assert_exact(c, am, c_ref, am_ref)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "i32", "i64"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_random_shapes_value_only(sr, dt):
+    rng = np.random.default_rng(200 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in SHAPES:
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        c, _ = gpu_gemm(sr, a, b, False)
+        c_ref, _ = oracle.gemm(sr, a, b, with_argmax=False)
+        assert_exact(c, None, c_ref, None)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_column_major_layout(sr):
+    rng = np.random.default_rng(9)
+    for dtype in (np.float32, np.int64):
+        a = tc.rng_matrix(rng, dtype, (45, 77), -50, 50)
+        b = tc.rng_matrix(rng, dtype, (77, 29), -50, 50)
+        c_ref, am_ref = oracle.gemm(sr, a, b)
+        for api in ("alloc", "ws"):
+            c, am = gpu_gemm(sr, a, b, True, layout="col", api=api)
+            assert_exact(c, am, c_ref, am_ref)
+            c, _ = gpu_gemm(sr, a, b, False, layout="col", api=api)
+            assert_exact(c, None, c_ref, None)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+def test_heavy_ties_first_k(sr, dt):
+    # Values in {0,1,2}: most outputs have many maximisers spread over chunks.
+    rng = np.random.default_rng(77)
+    dtype = tc.NP_DTYPES[dt]
+    a = rng.integers(0, 3, size=(150, 333)).astype(dtype)
+    b = rng.integers(0, 3, size=(333, 70)).astype(dtype)
+    c, am = gpu_gemm(sr, a, b)
+    c_ref, am_ref = oracle.gemm(sr, a, b)
+    assert_exact(c, am, c_ref, am_ref)
+
+
+def test_integer_wraparound_matches_cpu_semantics():
+    rng = np.random.default_rng(3)
+    for dtype in (np.int32, np.int64):
+        info = np.iinfo(dtype)
+        a = rng.integers(info.max - 50, info.max, size=(70, 90), dtype=dtype)
+        b = rng.integers(-5, 60, size=(90, 40)).astype(dtype)
+        for sr in tc.SEMIRINGS:
+            c, am = gpu_gemm(sr, a, b)
+            c_ref, am_ref = oracle.gemm(sr, a, b)
+            assert_exact(c, am, c_ref, am_ref)
+
+
+def test_special_values():
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((80, 96)).astype(np.float32)
+    b = rng.standard_normal((96, 72)).astype(np.float32)
+    a[rng.random(a.shape) < 0.2] = np.inf
+    b[rng.random(b.shape) < 0.2] = np.inf
+    c, am = gpu_gemm("minplus", a, b)
+    assert_exact(c, am, *oracle.gemm("minplus", a, b))
+    a2 = np.where(np.isinf(a), -np.inf, a).astype(np.float32)
+    b2 = np.where(np.isinf(b), -np.inf, b).astype(np.float32)
+    c, am = gpu_gemm("maxplus", a2, b2)
+    assert_exact(c, am, *oracle.gemm("maxplus", a2, b2))
+    # all-(-inf) rows: C = -inf, argmax 0
+    a2[3, :] = -np.inf
+    c, am = gpu_gemm("maxplus", a2, b2)
+    assert np.all(np.isneginf(c[3])) and np.all(am[3] == 0)
+    # MaxMul with zeros and negatives: products <= 0 never beat the zero.
+    a3 = rng.integers(-2, 3, size=(64, 50)).astype(np.float32)
+    b3 = rng.integers(-2, 3, size=(50, 64)).astype(np.float32)
+    c, am = gpu_gemm("maxmul", a3, b3)
+    assert_exact(c, am, *oracle.gemm("maxmul", a3, b3))
+
+
+def test_signed_zero_first_occurrence():
+    # -0 (k=0) and +0 (k=1..) tie at the maximum: the CPU keeps -0 / index 0.
+    a = np.zeros((4, 70), np.float32)
+    a[:, 0] = -0.0
+    b = np.zeros((70, 5), np.float32)
+    b[0, :] = -0.0
+    b[1:, :] = -1.0
+    b[40, :] = 0.0
+    c, am = gpu_gemm("maxplus", a, b)
+    c_ref, am_ref = oracle.gemm("maxplus", a, b)
+    assert_exact(c, am, c_ref, am_ref)
+    assert np.all(np.signbit(c)) and np.all(am == 0)
+
+
+def test_k_zero_and_empty():
+    for sr, z in [("maxplus", -np.inf), ("minplus", np.inf), ("maxmul", 0.0)]:
+        c, am = gpu_gemm(sr, np.zeros((5, 0), np.float32), np.zeros((0, 3), np.float32))
+        assert np.all(c == z) and np.all(am == 0)
+    c, am = gpu_gemm("maxplus", np.zeros((0, 4), np.float32), np.zeros((4, 3), np.float32))
+    assert c.shape == (0, 3)
+
+
+def test_unaligned_and_odd_strides_use_scalar_path():
+    # K, N not multiples of 4 -> scalar tile loads; offset pointers -> unaligned.
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    rng = np.random.default_rng(8)
+    m, k, n = 70, 45, 53
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    ta = _dev(np.concatenate([[0.0], a.ravel()]).astype(np.float32))
+    tb = _dev(np.concatenate([[0.0], b.ravel()]).astype(np.float32))
+    c = torch.empty(m * n, dtype=torch.float32, device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm(0, 0, 0, 0, ctypes.c_void_p(ta.data_ptr() + 4),
+                          ctypes.c_void_p(tb.data_ptr() + 4), _p(c), _p(am), m, n, k, None))
+    torch.cuda.synchronize()
+    assert_exact(c.cpu().numpy().reshape(m, n), am.cpu().numpy().reshape(m, n),
+                 *oracle.gemm("maxplus", a, b))
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_strided_batched_with_gaps(sr):
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    rng = np.random.default_rng(12)
+    batch, m, k, n = 3, 33, 70, 41
+    sa, sb, sc = m * k + 5, k * n + 3, m * n + 7
+    a = rng.standard_normal(batch * sa).astype(np.float32)
+    b = rng.standard_normal(batch * sb).astype(np.float32)
+    ta, tb = _dev(a), _dev(b)
+    c = torch.zeros(batch * sc, dtype=torch.float32, device=DEV)
+    am = torch.zeros(batch * sc, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm_strided_batched(0, nat.SEMIRING[sr], 0, 0, _p(ta), _p(tb), _p(c), _p(am),
+                                          batch, m, n, k, sa, sb, sc, None))
+    torch.cuda.synchronize()
+    c_np, am_np = c.cpu().numpy(), am.cpu().numpy()
+    for t in range(batch):
+        at = a[t * sa: t * sa + m * k].reshape(m, k)
+        bt = b[t * sb: t * sb + k * n].reshape(k, n)
+        c_ref, am_ref = oracle.gemm(sr, at, bt)
+        assert_exact(c_np[t * sc: t * sc + m * n].reshape(m, n),
+                     am_np[t * sc: t * sc + m * n].reshape(m, n), c_ref, am_ref)
+
+
+def test_device_out_of_range_is_dimension_mismatch():
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    n = nat.device_count()
+    t = torch.zeros(16, device=DEV)
+    rc = lib.tg_gemm(n + 3, 0, 0, 0, _p(t), _p(t), _p(t), None, 2, 2, 2, None)
+    assert rc == nat.TG_ERR_DIMENSION_MISMATCH and "not available" in nat.last_error()
+
+
+def test_context_and_memory_entry_points():
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    nat.check(lib.tg_context_init(0))
+    buf = ctypes.create_string_buffer(256)
+    nat.check(lib.tg_device_name(0, buf, 256))
+    assert b"gfx950" in buf.value
+    ptr = ctypes.c_void_p()
+    nat.check(lib.tg_malloc(0, ctypes.byref(ptr), 4096))
+    host = np.arange(1024, dtype=np.float32)
+    back = np.zeros_like(host)
+    nat.check(lib.tg_memcpy_htod(0, ptr, host.ctypes.data_as(ctypes.c_void_p), host.nbytes))
+    nat.check(lib.tg_memset_zero(0, ptr, 100, None))
+    nat.check(lib.tg_synchronize(0))
+    nat.check(lib.tg_memcpy_dtoh(0, back.ctypes.data_as(ctypes.c_void_p), ptr, host.nbytes))
+    assert np.all(back[:25] == 0) and np.array_equal(back[25:], host[25:])
+    nat.check(lib.tg_free(0, ptr))

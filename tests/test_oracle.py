@@ -1,0 +1,181 @@
+"""Pins the CPU oracle (oracle/tg_oracle.c) before anything is checked against it.
+
+* every golden fixture the reference ships (values bit-exact, argmax exact);
+* the reference's hand-computed cases (tie rule, -inf identity, K = 0);
+* an independent brute-force numpy formulation on random small shapes for
+  all dtypes and semirings, including heavy ties and integer wrap-around;
+* the backward loops against closed forms and np.add.at;
+* the single-thread baseline restatement against the oracle.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests import tg_cases as tc
+
+
+@pytest.mark.parametrize("path", tc.fixture_paths(), ids=lambda p: p.split("fixtures/")[-1])
+def test_oracle_matches_golden_fixture(path):
+    fx = tc.load_fixture(path)
+    if fx["a"].ndim == 3:
+        c, am = oracle.gemm_batched(fx["algebra"], fx["a"], fx["b"])
+    else:
+        c, am = oracle.gemm(fx["algebra"], fx["a"], fx["b"])
+    np.testing.assert_array_equal(tc.bits(c), tc.bits(fx["c"]))
+    np.testing.assert_array_equal(am.astype(np.int64), fx["argmax"])
+
+
+def test_fixture_inventory():
+    # 3 algebras x 2 float dtypes x (5 shapes + 2 batched) + 6 special cases.
+    assert len(tc.fixture_paths()) == 48
+
+
+@pytest.mark.parametrize("case", tc.HAND_CASES, ids=lambda c: c[5])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_oracle_hand_cases(case, dtype):
+    sr, a, b, c_exp, am_exp, _src = case
+    c, am = oracle.gemm(sr, a.astype(dtype), b.astype(dtype))
+    np.testing.assert_array_equal(c, np.array(c_exp, dtype=dtype))
+    np.testing.assert_array_equal(am, np.array(am_exp))
+
+
+@pytest.mark.parametrize("dtype", [np.int32, np.int64])
+def test_oracle_integer_hand_cases(dtype):
+    # tropical-gemm/src/api.rs:918-957 (i32/i64 MaxPlus and MinPlus).
+    a = np.arange(1, 7, dtype=dtype).reshape(2, 3)
+    b = np.arange(1, 7, dtype=dtype).reshape(3, 2)
+    c, _ = oracle.gemm("maxplus", a, b)
+    np.testing.assert_array_equal(c, [[8, 9], [11, 12]])
+    c, _ = oracle.gemm("minplus", a, b)
+    np.testing.assert_array_equal(c, [[2, 3], [5, 6]])
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+@pytest.mark.parametrize("dt", ["f32", "f64", "i32", "i64"])
+def test_oracle_matches_brute_force(sr, dt):
+    rng = np.random.default_rng(1234 + hash((sr, dt)) % 1000)
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in [(1, 1, 1), (3, 5, 7), (17, 33, 9), (40, 70, 31)]:
+        a = tc.rng_matrix(rng, dtype, (m, k), -20, 20)
+        b = tc.rng_matrix(rng, dtype, (k, n), -20, 20)
+        c, am = oracle.gemm(sr, a, b)
+        c_bf, am_bf = tc.brute_force(sr, a, b)
+        np.testing.assert_array_equal(tc.bits(c), tc.bits(c_bf))
+        np.testing.assert_array_equal(am.astype(np.int64), am_bf)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_oracle_ties_first_k(sr):
+    # Few distinct values -> most outputs have several maximisers.
+    rng = np.random.default_rng(7)
+    a = rng.integers(0, 3, size=(23, 41)).astype(np.float32)
+    b = rng.integers(0, 3, size=(41, 19)).astype(np.float32)
+    c, am = oracle.gemm(sr, a, b)
+    c_bf, am_bf = tc.brute_force(sr, a, b)
+    np.testing.assert_array_equal(c, c_bf)
+    np.testing.assert_array_equal(am.astype(np.int64), am_bf)
+
+
+def test_oracle_integer_wraps():
+    # Release-build Rust `+` wraps (types/scalar.rs:94-102).
+    a = np.array([[2**31 - 1, 5]], dtype=np.int32)
+    b = np.array([[1], [2]], dtype=np.int32)
+    c, am = oracle.gemm("maxplus", a, b)
+    # 2^31-1 + 1 wraps to -2^31, so k = 1 (5 + 2 = 7) wins.
+    assert c[0, 0] == 7 and am[0, 0] == 1
+    c, am = oracle.gemm("minplus", a, b)
+    assert c[0, 0] == -(2**31) and am[0, 0] == 0
+
+
+def test_oracle_k_zero_gives_tropical_zero():
+    for sr, z in [("maxplus", -np.inf), ("minplus", np.inf), ("maxmul", 0.0)]:
+        c, am = oracle.gemm(sr, np.zeros((3, 0), np.float32), np.zeros((0, 4), np.float32))
+        assert np.all(c == z) and np.all(am == 0)
+
+
+def test_oracle_special_values():
+    # MinPlus with +inf entries (test_tropical_gemm.py:529-538): inf never wins.
+    a = np.array([[np.inf, 1.0], [2.0, np.inf]], dtype=np.float32)
+    b = np.array([[1.0, np.inf], [np.inf, 3.0]], dtype=np.float32)
+    c, am = oracle.gemm("minplus", a, b)
+    np.testing.assert_array_equal(c, [[np.inf, 4.0], [3.0, np.inf]])
+    np.testing.assert_array_equal(am, [[0, 1], [0, 0]])
+    # MaxMul with zeros (test_tropical_gemm.py:541-554): all products <= 0 keep (0, 0).
+    a = np.array([[0.0, -1.0]], dtype=np.float32)
+    b = np.array([[5.0], [2.0]], dtype=np.float32)
+    c, am = oracle.gemm("maxmul", a, b)
+    assert c[0, 0] == 0.0 and am[0, 0] == 0
+
+
+def test_oracle_signed_zero_first_occurrence():
+    # Select rule keeps the earlier of equal values: -0 then +0 stays -0.
+    a = np.array([[-0.0, 0.0]], dtype=np.float32)
+    b = np.array([[-0.0], [0.0]], dtype=np.float32)
+    c, am = oracle.gemm("maxplus", a, b)
+    assert np.signbit(c[0, 0]) and am[0, 0] == 0
+
+
+def _backward_ref(grad_c, argmax, k, other=None, which="a"):
+    m, n = grad_c.shape
+    out = np.zeros((m, k) if which == "a" else (k, n), dtype=np.float64)
+    ii, jj = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+    g = grad_c.astype(np.float64)
+    if other is not None:
+        g = g * (other[argmax, jj] if which == "a" else other[ii, argmax])
+    if which == "a":
+        np.add.at(out, (ii, argmax), g)
+    else:
+        np.add.at(out, (argmax, jj), g)
+    return out
+
+
+def test_oracle_backward_closed_forms():
+    # tropical-gemm/src/api.rs:1211-1260: all argmax = 2, grad_c = 1.
+    a = np.arange(1, 7, dtype=np.float64).reshape(2, 3)
+    b = np.arange(1, 7, dtype=np.float64).reshape(3, 2)
+    _, am = oracle.gemm("maxplus", a, b)
+    g = np.ones((2, 2))
+    ga = oracle.backward_a(g, am, 3)
+    gb = oracle.backward_b(g, am, 3)
+    np.testing.assert_array_equal(ga, [[0, 0, 2], [0, 0, 2]])
+    np.testing.assert_array_equal(gb, [[0, 0], [0, 0], [2, 2]])
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("mult", [False, True])
+def test_oracle_backward_matches_add_at(dtype, mult):
+    rng = np.random.default_rng(5)
+    m, k, n = 37, 23, 29
+    a = rng.standard_normal((m, k)).astype(dtype)
+    b = rng.standard_normal((k, n)).astype(dtype)
+    _, am = oracle.gemm("maxmul" if mult else "maxplus", a, b)
+    g = rng.standard_normal((m, n)).astype(dtype)
+    ga = oracle.backward_a(g, am, k, b if mult else None)
+    gb = oracle.backward_b(g, am, k, a if mult else None)
+    tol = 1e-5 if dtype == np.float32 else 1e-12
+    np.testing.assert_allclose(ga, _backward_ref(g, am.astype(np.int64), k, b if mult else None, "a"),
+                               rtol=tol, atol=tol)
+    np.testing.assert_allclose(gb, _backward_ref(g, am.astype(np.int64), k, a if mult else None, "b"),
+                               rtol=tol, atol=tol)
+    if not mult:
+        # Invariant: every upstream gradient lands exactly once (api.rs:1295-1298).
+        assert abs(ga.sum(dtype=np.float64) - g.sum(dtype=np.float64)) < 1e-3
+        assert abs(gb.sum(dtype=np.float64) - g.sum(dtype=np.float64)) < 1e-3
+
+
+def test_oracle_backward_skips_out_of_range_index():
+    g = np.ones((1, 2), np.float32)
+    am = np.array([[0, 7]], dtype=np.uint32)  # 7 >= k: skipped (api.rs:575-582)
+    ga = oracle.backward_a(g, am, 3)
+    np.testing.assert_array_equal(ga, [[1, 0, 0]])
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_portable_baseline_equals_oracle(sr):
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((67, 301)).astype(np.float32)
+    b = rng.standard_normal((301, 130)).astype(np.float32)
+    c1, a1 = oracle.gemm(sr, a, b)
+    c2, a2 = oracle.portable_argmax_f32(sr, a, b)
+    np.testing.assert_array_equal(tc.bits(c1), tc.bits(c2))
+    np.testing.assert_array_equal(a1, a2)

@@ -1,0 +1,626 @@
+// tg_capi.hip -- the C ABI declared in include/tropical_gemm_hip.h.
+//
+// Host side of the drop-in boundary: argument validation (done before any HIP
+// call, so it is testable without a GPU), device selection, layout mapping,
+// workspace handling and kernel dispatch.  Reference counterparts are cited
+// per entry point in the header.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/tropical_gemm_hip.h"
+#include "tg_kernels.hpp"
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+thread_local std::string g_last_error = "";
+
+int fail(int status, const std::string& msg) {
+    g_last_error = msg;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(TG_ERR_DRIVER, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define TG_HIP(expr)                                   \
+    do {                                               \
+        hipError_t _e = (expr);                        \
+        if (_e != hipSuccess) return hip_fail(_e, #expr); \
+    } while (0)
+
+int elem_size(tg_dtype dt) {
+    switch (dt) {
+        case TG_F32:
+        case TG_I32:
+            return 4;
+        case TG_F64:
+        case TG_I64:
+            return 8;
+    }
+    return 0;
+}
+
+const char* dtype_name(int dt) {
+    switch (dt) {
+        case TG_F32: return "f32";
+        case TG_F64: return "f64";
+        case TG_I32: return "i32";
+        case TG_I64: return "i64";
+    }
+    return "?";
+}
+
+bool valid_semiring(int s) { return s == TG_MAXPLUS || s == TG_MINPLUS || s == TG_MAXMUL; }
+bool valid_dtype(int d) { return d == TG_F32 || d == TG_F64 || d == TG_I32 || d == TG_I64; }
+bool valid_layout(int l) { return l == TG_ROW_MAJOR || l == TG_COL_MAJOR; }
+
+// Device handling: the ordinal is validated against the device count (the
+// reference answers an out-of-range ordinal with DimensionMismatch,
+// crates/tropical-gemm-cuda/src/lib.rs:81-87) and made current.
+std::once_flag g_count_once;
+int g_device_count = -1;
+hipError_t g_count_err = hipSuccess;
+
+int device_count_cached(int* out) {
+    std::call_once(g_count_once, [] {
+        int n = 0;
+        g_count_err = hipGetDeviceCount(&n);
+        g_device_count = (g_count_err == hipSuccess) ? n : 0;
+    });
+    if (g_count_err != hipSuccess && g_count_err != hipErrorNoDevice)
+        return hip_fail(g_count_err, "hipGetDeviceCount");
+    *out = g_device_count;
+    return TG_OK;
+}
+
+int select_device(int device) {
+    int n = 0;
+    int rc = device_count_cached(&n);
+    if (rc != TG_OK) return rc;
+    if (n <= 0) return fail(TG_ERR_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "Device " + std::to_string(device) +
+                                                   " not available (only " + std::to_string(n) +
+                                                   " HIP device(s) found)");
+    int cur = -1;
+    TG_HIP(hipGetDevice(&cur));
+    if (cur != device) TG_HIP(hipSetDevice(device));
+    return TG_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ----------------------------------------------------------------------------
+// Launch helpers
+// ----------------------------------------------------------------------------
+
+int launch_fill_zero(void* p, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return TG_OK;
+    int64_t nvec = int64_t(bytes / 16);
+    int64_t blocks = (nvec + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(tg::tg_fill_zero, dim3(unsigned(blocks)), dim3(256), 0, st,
+                       static_cast<unsigned char*>(p), int64_t(bytes));
+    TG_HIP(hipGetLastError());
+    return TG_OK;
+}
+
+template <typename T>
+bool aligned16(const void* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Row-major problem description after the layout mapping.
+struct Problem {
+    const void* A;
+    const void* B;
+    void* C;
+    int32_t* IDX;
+    int64_t batch, M, N, K, sA, sB, sC;
+};
+
+template <int SR, typename T>
+int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
+    using Cfg = tg::TileCfg<T>;
+    const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    if (tiles_m * tiles_n > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    const T* A = static_cast<const T*>(p.A);
+    const T* B = static_cast<const T*>(p.B);
+    T* C = static_cast<T*>(p.C);
+    constexpr int VW = 16 / int(sizeof(T));
+    const bool vec = (p.K % VW == 0) && (p.N % VW == 0) && (p.sA % VW == 0) &&
+                     (p.sB % VW == 0) && aligned16<T>(A) && aligned16<T>(B);
+    const bool argmax = p.IDX != nullptr;
+
+    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+        const T* Az = A + z0 * p.sA;
+        const T* Bz = B + z0 * p.sB;
+        T* Cz = C + z0 * p.sC;
+        int32_t* Iz = argmax ? p.IDX + z0 * p.sC : nullptr;
+        dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+        if (argmax) {
+            if (vec)
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true>), grid, dim3(256), 0, st,
+                                   Az, Bz, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                                   int(tiles_n));
+            else
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false>), grid, dim3(256), 0, st,
+                                   Az, Bz, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                                   int(tiles_n));
+            TG_HIP(hipGetLastError());
+            // Resolve the exact first-k index inside each winning chunk.
+            T* BT = static_cast<T*>(ws) + 0;
+            const int64_t sBT = p.K * p.N;
+            if (p.K > 0) {
+                dim3 tg_grid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+                if ((p.K + 31) / 32 > 65535)
+                    return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
+                hipLaunchKernelGGL((tg::tg_transpose<T>), tg_grid, dim3(32, 8), 0, st, Bz, BT,
+                                   p.K, p.N, p.sB, sBT);
+                TG_HIP(hipGetLastError());
+            }
+            const int64_t outs = p.M * p.N;
+            const int64_t blocks = (outs + 255) / 256;
+            if (blocks > 0x7fffffffLL) return fail(TG_ERR_DIMENSION_MISMATCH, "output too large");
+            hipLaunchKernelGGL((tg::tg_resolve<SR, T>), dim3(unsigned(blocks), 1, unsigned(nb)),
+                               dim3(256), 0, st, Az, BT, Cz, Iz, p.M, p.N, p.K, p.sA, sBT, p.sC);
+            TG_HIP(hipGetLastError());
+        } else {
+            if (vec)
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, false, true>), grid, dim3(256), 0, st,
+                                   Az, Bz, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
+            else
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, false, false>), grid, dim3(256), 0,
+                                   st, Az, Bz, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
+            TG_HIP(hipGetLastError());
+        }
+    }
+    return TG_OK;
+}
+
+template <int SR>
+int run_gemm_sr(tg_dtype dt, const Problem& p, void* ws, hipStream_t st) {
+    switch (dt) {
+        case TG_F32: return run_gemm_typed<SR, float>(p, ws, st);
+        case TG_F64: return run_gemm_typed<SR, double>(p, ws, st);
+        case TG_I32: return run_gemm_typed<SR, int32_t>(p, ws, st);
+        case TG_I64: return run_gemm_typed<SR, int64_t>(p, ws, st);
+    }
+    return fail(TG_ERR_INVALID_ARGUMENT, "bad dtype");
+}
+
+int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, hipStream_t st) {
+    switch (sr) {
+        case TG_MAXPLUS: return run_gemm_sr<tg::SR_MAXPLUS>(dt, p, ws, st);
+        case TG_MINPLUS: return run_gemm_sr<tg::SR_MINPLUS>(dt, p, ws, st);
+        case TG_MAXMUL: return run_gemm_sr<tg::SR_MAXMUL>(dt, p, ws, st);
+    }
+    return fail(TG_ERR_INVALID_ARGUMENT, "bad semiring");
+}
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
+                           bool with_argmax) {
+    (void)m;
+    if (!with_argmax || batch <= 0 || n <= 0 || k <= 0) return 0;
+    return round_up(size_t(batch) * size_t(k) * size_t(n) * size_t(elem_size(dt)), 256);
+}
+
+// Validation shared by the forward entry points.  Returns TG_OK or an error.
+int validate_forward(int sr, int dt, int layout, const void* A, const void* B, const void* C,
+                     int64_t batch, int64_t m, int64_t n, int64_t k, int64_t sa, int64_t sb,
+                     int64_t sc, bool strided) {
+    if (!valid_semiring(sr)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown semiring " + std::to_string(sr));
+    if (!valid_dtype(dt)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown dtype " + std::to_string(dt));
+    if (!valid_layout(layout)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown layout " + std::to_string(layout));
+    if (batch < 0 || m < 0 || n < 0 || k < 0)
+        return fail(TG_ERR_DIMENSION_MISMATCH,
+                    "negative dimension: batch=" + std::to_string(batch) + " m=" + std::to_string(m) +
+                        " n=" + std::to_string(n) + " k=" + std::to_string(k));
+    if (m > 0x7fffffffLL || n > 0x7fffffffLL || k > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "dimension exceeds 2^31-1 (argmax is int32)");
+    const int64_t out = m * n;
+    if (batch > 0 && out > 0) {
+        if (C == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "C is NULL");
+        if (k > 0 && (A == nullptr || B == nullptr))
+            return fail(TG_ERR_INVALID_ARGUMENT, "A or B is NULL");
+    }
+    if (strided && batch > 1) {
+        if (sc < out)
+            return fail(TG_ERR_DIMENSION_MISMATCH,
+                        "stride_c (" + std::to_string(sc) + ") < m*n (" + std::to_string(out) +
+                            "): output matrices would overlap");
+        if (sa < 0 || sb < 0) return fail(TG_ERR_DIMENSION_MISMATCH, "negative input stride");
+    }
+    return TG_OK;
+}
+
+int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const void* A,
+              const void* B, void* C, int32_t* argmax, int64_t batch, int64_t m, int64_t n,
+              int64_t k, int64_t sa, int64_t sb, int64_t sc, bool strided, void* ws,
+              size_t ws_bytes, bool ws_given, void* stream) {
+    int rc = validate_forward(sr, dt, layout, A, B, C, batch, m, n, k, sa, sb, sc, strided);
+    if (rc != TG_OK) return rc;
+    const bool with_argmax = argmax != nullptr;
+    const size_t need = workspace_bytes_for(dt, batch, m, n, k, with_argmax);
+    if (ws_given && need > 0) {
+        if (ws == nullptr || ws_bytes < need)
+            return fail(TG_ERR_INVALID_ARGUMENT, "workspace too small: need " + std::to_string(need) +
+                                                     " bytes, got " + std::to_string(ws_bytes));
+        if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+            return fail(TG_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+    }
+    rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    if (batch == 0 || m == 0 || n == 0) return TG_OK;
+    hipStream_t st = as_stream(stream);
+
+    // Layout mapping: a column-major product C = A (x) B is the row-major
+    // product C^T = B^T (x) A^T over the same buffers (kernels.rs:370-430).
+    Problem p;
+    if (layout == TG_ROW_MAJOR) {
+        p = Problem{A, B, C, argmax, batch, m, n, k, sa, sb, sc};
+    } else {
+        p = Problem{B, A, C, argmax, batch, n, m, k, sb, sa, sc};
+    }
+    if (!strided) {
+        p.sA = p.M * p.K;
+        p.sB = p.K * p.N;
+        p.sC = p.M * p.N;
+    }
+
+    void* work = ws;
+    bool own = false;
+    if (need > 0 && !ws_given) {
+        TG_HIP(hipMallocAsync(&work, need, st));
+        own = true;
+    }
+    rc = run_gemm(sr, dt, p, work, st);
+    if (own) {
+        hipError_t e = hipFreeAsync(work, st);
+        if (rc == TG_OK && e != hipSuccess) return hip_fail(e, "hipFreeAsync");
+    }
+    return rc;
+}
+
+// ----------------------------------------------------------------------------
+// Backward
+// ----------------------------------------------------------------------------
+
+constexpr size_t kRowLdsLimit = 64 * 1024;
+
+template <typename T, bool MULT>
+int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t batch, int64_t M,
+                      int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sA, hipStream_t st) {
+    for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
+        const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
+        const T* Gz = G + z0 * sC;
+        const int32_t* Iz = I + z0 * sC;
+        const T* Oz = MULT ? O + z0 * sO : nullptr;
+        T* GAz = GA + z0 * sA;
+        const size_t lds = size_t(K) * sizeof(T);
+        if (lds <= kRowLdsLimit && M <= 0x7fffffffLL) {
+            hipLaunchKernelGGL((tg::tg_backward_rows<T, MULT>), dim3(unsigned(M), 1, unsigned(nb)),
+                               dim3(256), lds, st, Gz, Iz, Oz, GAz, M, N, K, sC, sO, sA);
+            TG_HIP(hipGetLastError());
+        } else {
+            for (int64_t z = 0; z < nb; ++z) {
+                int rc = launch_fill_zero(GAz + z * sA, size_t(M * K) * sizeof(T), st);
+                if (rc != TG_OK) return rc;
+            }
+            const int64_t blocks = (M * N + 255) / 256;
+            hipLaunchKernelGGL((tg::tg_backward_rows_global<T, MULT>),
+                               dim3(unsigned(blocks), 1, unsigned(nb)), dim3(256), 0, st, Gz, Iz,
+                               Oz, GAz, M, N, K, sC, sO, sA);
+            TG_HIP(hipGetLastError());
+        }
+    }
+    return TG_OK;
+}
+
+template <typename T, bool MULT>
+int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t batch, int64_t M,
+                      int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sB, hipStream_t st) {
+    for (int64_t z = 0; z < batch; ++z) {
+        int rc = launch_fill_zero(GB + z * sB, size_t(K * N) * sizeof(T), st);
+        if (rc != TG_OK) return rc;
+    }
+    if (M * N == 0) return TG_OK;
+    for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
+        const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
+        const int64_t blocks = (M * N + 255) / 256;
+        hipLaunchKernelGGL((tg::tg_backward_cols<T, MULT>), dim3(unsigned(blocks), 1, unsigned(nb)),
+                           dim3(256), 0, st, G + z0 * sC, I + z0 * sC,
+                           MULT ? O + z0 * sO : nullptr, GB + z0 * sB, M, N, K, sC, sO, sB);
+        TG_HIP(hipGetLastError());
+    }
+    return TG_OK;
+}
+
+// which: 0 = grad wrt the left operand (rows of C), 1 = wrt the right operand.
+// Operates on the row-major problem.
+template <typename T>
+int run_backward_typed(int which, bool mult, const void* G, const int32_t* I, const void* O,
+                       void* OUT, int64_t batch, int64_t M, int64_t N, int64_t K, int64_t sC,
+                       int64_t sO, int64_t sOut, hipStream_t st) {
+    const T* g = static_cast<const T*>(G);
+    const T* o = static_cast<const T*>(O);
+    T* out = static_cast<T*>(OUT);
+    if (which == 0) {
+        if (mult) return run_backward_rows<T, true>(g, I, o, out, batch, M, N, K, sC, sO, sOut, st);
+        return run_backward_rows<T, false>(g, I, o, out, batch, M, N, K, sC, sO, sOut, st);
+    }
+    if (mult) return run_backward_cols<T, true>(g, I, o, out, batch, M, N, K, sC, sO, sOut, st);
+    return run_backward_cols<T, false>(g, I, o, out, batch, M, N, K, sC, sO, sOut, st);
+}
+
+// Public-level backward: `want_a` selects grad wrt A (else B); `other` is B
+// (for grad A) or A (for grad B) under the MaxMul rule, NULL otherwise.
+int backward_impl(int device, tg_dtype dt, tg_layout layout, bool want_a, const void* grad_c,
+                  const int32_t* argmax, const void* other, void* out, int64_t batch, int64_t m,
+                  int64_t n, int64_t k, int64_t s_c, int64_t s_other, int64_t s_out, bool strided,
+                  bool mult, void* stream) {
+    if (!valid_dtype(dt)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown dtype " + std::to_string(dt));
+    if (dt != TG_F32 && dt != TG_F64)
+        return fail(TG_ERR_UNSUPPORTED, std::string("backward is defined for f32/f64 only, got ") +
+                                            dtype_name(dt));
+    if (!valid_layout(layout)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown layout " + std::to_string(layout));
+    if (batch < 0 || m < 0 || n < 0 || k < 0) return fail(TG_ERR_DIMENSION_MISMATCH, "negative dimension");
+    if (m > 0x7fffffffLL || n > 0x7fffffffLL || k > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "dimension exceeds 2^31-1");
+    const int64_t out_elems = want_a ? m * k : k * n;
+    if (batch > 0 && out_elems > 0 && out == nullptr)
+        return fail(TG_ERR_INVALID_ARGUMENT, "gradient output is NULL");
+    if (batch > 0 && m * n > 0 && (grad_c == nullptr || argmax == nullptr))
+        return fail(TG_ERR_INVALID_ARGUMENT, "grad_c or argmax is NULL");
+    if (mult && batch > 0 && m * n > 0 && k > 0 && other == nullptr)
+        return fail(TG_ERR_INVALID_ARGUMENT, "MaxMul backward needs the other operand");
+    if (strided && batch > 1) {
+        if (s_out < out_elems)
+            return fail(TG_ERR_DIMENSION_MISMATCH, "gradient stride smaller than one matrix");
+        if (s_c < 0 || s_other < 0) return fail(TG_ERR_DIMENSION_MISMATCH, "negative stride");
+    }
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    if (batch == 0 || out_elems == 0) return TG_OK;
+    if (!strided) {
+        s_c = m * n;
+        s_other = want_a ? k * n : m * k;
+        s_out = out_elems;
+    }
+    hipStream_t st = as_stream(stream);
+    // Row-major problem C (M x N) = L (M x K) (x) R (K x N).  Column-major
+    // data is the row-major transposed problem C^T = B^T (x) A^T, in which
+    // A's gradient is the right operand's gradient and vice versa.
+    int which;
+    int64_t M, N;
+    if (layout == TG_ROW_MAJOR) {
+        which = want_a ? 0 : 1;
+        M = m;
+        N = n;
+    } else {
+        which = want_a ? 1 : 0;
+        M = n;
+        N = m;
+    }
+    if (dt == TG_F32)
+        return run_backward_typed<float>(which, mult, grad_c, argmax, other, out, batch, M, N, k,
+                                         s_c, s_other, s_out, st);
+    return run_backward_typed<double>(which, mult, grad_c, argmax, other, out, batch, M, N, k, s_c,
+                                      s_other, s_out, st);
+}
+
+}  // namespace
+
+// ============================================================================
+// Exported C ABI
+// ============================================================================
+
+extern "C" {
+
+int tg_version(void) { return kAbiVersion; }
+
+const char* tg_status_string(int status) {
+    switch (status) {
+        case TG_OK: return "success";
+        case TG_ERR_DRIVER: return "HIP driver/runtime error";
+        case TG_ERR_COMPILE: return "kernel compilation error";
+        case TG_ERR_NO_DEVICE: return "no HIP device available";
+        case TG_ERR_DIMENSION_MISMATCH: return "dimension mismatch";
+        case TG_ERR_KERNEL_NOT_FOUND: return "kernel not found";
+        case TG_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case TG_ERR_UNSUPPORTED: return "unsupported operation";
+    }
+    return "unknown status";
+}
+
+const char* tg_last_error(void) { return g_last_error.c_str(); }
+
+int tg_device_count(int* count) {
+    if (count == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "count is NULL");
+    return device_count_cached(count);
+}
+
+int tg_context_init(int device) {
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipFree(nullptr));  // forces runtime/context initialisation
+    return TG_OK;
+}
+
+int tg_device_name(int device, char* buf, size_t len) {
+    if (buf == nullptr || len == 0) return fail(TG_ERR_INVALID_ARGUMENT, "buffer is NULL");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    hipDeviceProp_t prop;
+    TG_HIP(hipGetDeviceProperties(&prop, device));
+    std::snprintf(buf, len, "HIP Device %d (%s, %s)", device, prop.name, prop.gcnArchName);
+    return TG_OK;
+}
+
+int tg_malloc(int device, void** ptr, size_t bytes) {
+    if (ptr == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "ptr is NULL");
+    *ptr = nullptr;
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    if (bytes == 0) return TG_OK;
+    TG_HIP(hipMalloc(ptr, bytes));
+    return TG_OK;
+}
+
+int tg_free(int device, void* ptr) {
+    if (ptr == nullptr) return TG_OK;
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipFree(ptr));
+    return TG_OK;
+}
+
+int tg_memcpy_htod(int device, void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return TG_OK;
+    if (dst == nullptr || src == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "NULL pointer");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return TG_OK;
+}
+
+int tg_memcpy_dtoh(int device, void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return TG_OK;
+    if (dst == nullptr || src == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "NULL pointer");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return TG_OK;
+}
+
+int tg_memcpy_dtod(int device, void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return TG_OK;
+    if (dst == nullptr || src == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "NULL pointer");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return TG_OK;
+}
+
+int tg_memset_zero(int device, void* ptr, size_t bytes, void* stream) {
+    if (bytes == 0) return TG_OK;
+    if (ptr == nullptr) return fail(TG_ERR_INVALID_ARGUMENT, "ptr is NULL");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    return launch_fill_zero(ptr, bytes, as_stream(stream));
+}
+
+int tg_synchronize(int device) {
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipDeviceSynchronize());
+    return TG_OK;
+}
+
+int tg_stream_synchronize(int device, void* stream) {
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipStreamSynchronize(as_stream(stream)));
+    return TG_OK;
+}
+
+int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout, const void* A,
+            const void* B, void* C, int32_t* argmax, int64_t m, int64_t n, int64_t k,
+            void* stream) {
+    return gemm_impl(device, semiring, dtype, layout, A, B, C, argmax, 1, m, n, k, 0, 0, 0, false,
+                     nullptr, 0, false, stream);
+}
+
+size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,
+                              int with_argmax) {
+    if (!valid_dtype(dtype)) return 0;
+    return workspace_bytes_for(dtype, batch, m, n, k, with_argmax != 0);
+}
+
+int tg_gemm_ws(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout, const void* A,
+               const void* B, void* C, int32_t* argmax, int64_t m, int64_t n, int64_t k,
+               void* workspace, size_t workspace_bytes, void* stream) {
+    return gemm_impl(device, semiring, dtype, layout, A, B, C, argmax, 1, m, n, k, 0, 0, 0, false,
+                     workspace, workspace_bytes, true, stream);
+}
+
+int tg_gemm_strided_batched(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                            const void* A, const void* B, void* C, int32_t* argmax, int64_t batch,
+                            int64_t m, int64_t n, int64_t k, int64_t stride_a, int64_t stride_b,
+                            int64_t stride_c, void* stream) {
+    return gemm_impl(device, semiring, dtype, layout, A, B, C, argmax, batch, m, n, k, stride_a,
+                     stride_b, stride_c, true, nullptr, 0, false, stream);
+}
+
+int tg_gemm_strided_batched_ws(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                               const void* A, const void* B, void* C, int32_t* argmax,
+                               int64_t batch, int64_t m, int64_t n, int64_t k, int64_t stride_a,
+                               int64_t stride_b, int64_t stride_c, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    return gemm_impl(device, semiring, dtype, layout, A, B, C, argmax, batch, m, n, k, stride_a,
+                     stride_b, stride_c, true, workspace, workspace_bytes, true, stream);
+}
+
+int tg_backward_a(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
+                  const int32_t* argmax, void* grad_a, int64_t m, int64_t n, int64_t k,
+                  void* stream) {
+    return backward_impl(device, dtype, layout, true, grad_c, argmax, nullptr, grad_a, 1, m, n, k,
+                         0, 0, 0, false, false, stream);
+}
+
+int tg_backward_b(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
+                  const int32_t* argmax, void* grad_b, int64_t m, int64_t n, int64_t k,
+                  void* stream) {
+    return backward_impl(device, dtype, layout, false, grad_c, argmax, nullptr, grad_b, 1, m, n, k,
+                         0, 0, 0, false, false, stream);
+}
+
+int tg_maxmul_backward_a(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
+                         const int32_t* argmax, const void* B, void* grad_a, int64_t m, int64_t n,
+                         int64_t k, void* stream) {
+    return backward_impl(device, dtype, layout, true, grad_c, argmax, B, grad_a, 1, m, n, k, 0, 0,
+                         0, false, true, stream);
+}
+
+int tg_maxmul_backward_b(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
+                         const int32_t* argmax, const void* A, void* grad_b, int64_t m, int64_t n,
+                         int64_t k, void* stream) {
+    return backward_impl(device, dtype, layout, false, grad_c, argmax, A, grad_b, 1, m, n, k, 0, 0,
+                         0, false, true, stream);
+}
+
+int tg_backward_a_strided_batched(int device, tg_dtype dtype, tg_layout layout,
+                                  const void* grad_c, const int32_t* argmax, const void* other,
+                                  void* grad_a, int64_t batch, int64_t m, int64_t n, int64_t k,
+                                  int64_t stride_c, int64_t stride_other, int64_t stride_a,
+                                  void* stream) {
+    return backward_impl(device, dtype, layout, true, grad_c, argmax, other, grad_a, batch, m, n, k,
+                         stride_c, stride_other, stride_a, true, other != nullptr, stream);
+}
+
+int tg_backward_b_strided_batched(int device, tg_dtype dtype, tg_layout layout,
+                                  const void* grad_c, const int32_t* argmax, const void* other,
+                                  void* grad_b, int64_t batch, int64_t m, int64_t n, int64_t k,
+                                  int64_t stride_c, int64_t stride_other, int64_t stride_b,
+                                  void* stream) {
+    return backward_impl(device, dtype, layout, false, grad_c, argmax, other, grad_b, batch, m, n,
+                         k, stride_c, stride_other, stride_b, true, other != nullptr, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,460 @@
+// tg_kernels.hpp -- gfx950 kernels of the tropical GEMM path.
+//
+// Kernel map (reference kernel each one replaces, tropical_gemm.cu):
+//   tg_gemm_tiles      value-only and argmax GEMM for every dtype/semiring
+//                      (TROPICAL_GEMM_{F32,F64,I32,I64} 86-520,
+//                       TROPICAL_GEMM_ARGMAX_* 526-996, batched 1094-1219)
+//   tg_transpose       B -> B^T staging for the argmax resolve step (new)
+//   tg_resolve         exact first-k argmax inside the winning chunk (new)
+//   tg_backward_rows   grad_A scatter (TROPICAL_BACKWARD_A 1002-1018)
+//   tg_backward_cols   grad_B scatter (TROPICAL_BACKWARD_B 1020-1036)
+//   tg_fill_zero       zero fill used instead of hipMemsetAsync
+//
+// All matrices are row-major here; the host layer maps column-major calls
+// onto row-major ones with the operand swap C^T = B^T (x) A^T
+// (kernels.rs:370-430 does the same trick in the other direction).
+//
+// Argmax scheme ("chunked argmax").  K is cut into chunks of TG_CHUNK = 32
+// consecutive k (one LDS k-tile).  Inside a chunk each output folds products
+// with max/min only (two products per v_max3/v_min3).  At the chunk end one
+// compare against the value held before the chunk records the chunk index if
+// the chunk strictly improved it.  Because max/min select an operand exactly
+// and earlier chunks only lose on strict improvement, the first k attaining
+// the final value lies in the recorded chunk; tg_resolve finds it by
+// recomputing that chunk's <= 32 products (reading A and B^T rows) and takes
+// the first k whose product equals the final value, writing both the index
+// and that product's bits (so a -0/+0 tie keeps the first occurrence's sign,
+// exactly like the CPU select rule).  The per-(i,j,k) VALU cost is one
+// (x), half a max3 and 2/32 for the bookkeeping instead of the four
+// operations of a per-k compare-and-select.
+#pragma once
+
+#include "tg_device.hpp"
+
+namespace tg {
+
+constexpr int TG_CHUNK = 32;   // k per LDS tile == argmax chunk length
+constexpr int TG_THREADS = 256;
+
+// Tile shapes.  4-byte types: 128 x 64 output tile, 8 x 4 outputs per thread.
+// 8-byte types: 64 x 64 output tile, 4 x 4 outputs per thread.
+template <typename T>
+struct TileCfg;
+template <>
+struct TileCfg<float> {
+    static constexpr int BM = 128, BN = 64, TM = 8, TN = 4;
+};
+template <>
+struct TileCfg<int32_t> {
+    static constexpr int BM = 128, BN = 64, TM = 8, TN = 4;
+};
+template <>
+struct TileCfg<double> {
+    static constexpr int BM = 64, BN = 64, TM = 4, TN = 4;
+};
+template <>
+struct TileCfg<int64_t> {
+    static constexpr int BM = 64, BN = 64, TM = 4, TN = 4;
+};
+
+// 16-byte vector type of T (4 x 32-bit or 2 x 64-bit lanes).
+template <typename T>
+struct Vec16 {
+    static constexpr int N = 16 / sizeof(T);
+    T v[N];
+};
+
+// Block -> output tile.  Consecutive workgroup ids go round-robin over the 8
+// XCDs; remap so each XCD owns a contiguous range of tiles, then walk that
+// range in groups of 8 tile-rows so co-resident workgroups of one XCD share
+// A and B panels in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int total = tiles_m * tiles_n;
+    int lin = bid;
+    if ((total & 7) == 0) lin = (bid & 7) * (total >> 3) + (bid >> 3);
+    constexpr int GROUP = 8;
+    const int per_group = GROUP * tiles_n;
+    const int group = lin / per_group;
+    const int first_m = group * GROUP;
+    const int rem = tiles_m - first_m;
+    const int gsize = rem < GROUP ? rem : GROUP;
+    const int in_group = lin - group * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// Main GEMM kernel.
+//   ARGMAX=false : C = A (x) B.
+//   ARGMAX=true  : C = A (x) B and CH = winning chunk (or -1 when the tropical
+//                  zero was never beaten); tg_resolve turns CH into argmax.
+//   VEC          : K and N are multiples of 16/sizeof(T) and A, B are 16-byte
+//                  aligned, so tiles load with 16-byte global loads.
+// grid = (tiles_m * tiles_n, 1, batch), block = 256.
+// ---------------------------------------------------------------------------
+template <int SR, typename T, bool ARGMAX, bool VEC>
+__global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
+    const T* __restrict__ A, const T* __restrict__ B, T* __restrict__ C, int32_t* __restrict__ CH,
+    int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC, int tiles_m, int tiles_n) {
+    using Cfg = TileCfg<T>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, BK = TG_CHUNK;
+    constexpr int VW = Vec16<T>::N;          // elements per 16-byte vector
+    constexpr int PAD = VW;                  // keeps 16-byte alignment of LDS rows
+    constexpr int NVA = BM * BK / VW / TG_THREADS;  // 16-byte vectors of A per thread
+    constexpr int NVB = BK * BN / VW / TG_THREADS;  // 16-byte vectors of B per thread
+    static_assert(NVA >= 1 && NVB >= 1, "tile too small for the block");
+    static_assert(TM % 4 == 0 && TN % 4 == 0, "micro-tile must be made of 4-wide groups");
+
+    __shared__ __align__(16) T As[2][BK][BM + PAD];
+    __shared__ __align__(16) T Bs[2][BK][BN + PAD];
+
+    const int tid = threadIdx.x;
+    const int tx = tid & 15;
+    const int ty = tid >> 4;
+    int tm, tn;
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int64_t row0 = int64_t(tm) * BM;
+    const int64_t col0 = int64_t(tn) * BN;
+    const int64_t z = blockIdx.z;
+    A += z * sA;
+    B += z * sB;
+    C += z * sC;
+    if (ARGMAX) CH += z * sC;
+
+    // ---- global -> register staging ------------------------------------
+    Vec16<T> ra[NVA], rb[NVB];
+    auto load_tiles = [&](int64_t k0) {
+#pragma unroll
+        for (int v = 0; v < NVA; ++v) {
+            const int L = v * TG_THREADS + tid;
+            const int r = L / (BK / VW);
+            const int kq = (L % (BK / VW)) * VW;
+            const int64_t gr = row0 + r;
+            const int64_t gk = k0 + kq;
+            if constexpr (VEC) {
+                if (gr < M && gk < K) {
+                    ra[v] = *reinterpret_cast<const Vec16<T>*>(A + gr * K + gk);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) ra[v].v[e] = T(0);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VW; ++e)
+                    ra[v].v[e] = (gr < M && gk + e < K) ? A[gr * K + gk + e] : T(0);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < NVB; ++v) {
+            const int L = v * TG_THREADS + tid;
+            const int kr = L / (BN / VW);
+            const int nq = (L % (BN / VW)) * VW;
+            const int64_t gk = k0 + kr;
+            const int64_t gc = col0 + nq;
+            if constexpr (VEC) {
+                if (gk < K && gc < N) {
+                    rb[v] = *reinterpret_cast<const Vec16<T>*>(B + gk * N + gc);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) rb[v].v[e] = T(0);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < VW; ++e)
+                    rb[v].v[e] = (gk < K && gc + e < N) ? B[gk * N + gc + e] : T(0);
+            }
+        }
+    };
+    auto store_tiles = [&](int buf) {
+#pragma unroll
+        for (int v = 0; v < NVA; ++v) {
+            const int L = v * TG_THREADS + tid;
+            const int r = L / (BK / VW);
+            const int kq = (L % (BK / VW)) * VW;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) As[buf][kq + e][r] = ra[v].v[e];
+        }
+#pragma unroll
+        for (int v = 0; v < NVB; ++v) {
+            const int L = v * TG_THREADS + tid;
+            const int kr = L / (BN / VW);
+            const int nq = (L % (BN / VW)) * VW;
+            *reinterpret_cast<Vec16<T>*>(&Bs[buf][kr][nq]) = rb[v];
+        }
+    };
+
+    // ---- accumulators ------------------------------------------------------
+    T acc[TM][TN];
+    int32_t ch[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            acc[i][j] = tzero<SR, T>();
+            ch[i][j] = -1;
+        }
+
+    auto load_frag = [&](int buf, int kk, T (&a)[TM], T (&b)[TN]) {
+#pragma unroll
+        for (int g = 0; g < TM / 4; ++g) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[g * 4 + e] = As[buf][kk][g * 64 + ty * 4 + e];
+        }
+#pragma unroll
+        for (int g = 0; g < TN / 4; ++g) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) b[g * 4 + e] = Bs[buf][kk][g * 64 + tx * 4 + e];
+        }
+    };
+
+    const int64_t ntiles = (K + BK - 1) / BK;
+    if (ntiles > 0) {
+        load_tiles(0);
+        store_tiles(0);
+    }
+    __syncthreads();
+
+    for (int64_t t = 0; t < ntiles; ++t) {
+        const int buf = int(t & 1);
+        const int64_t k0 = t * BK;
+        if (t + 1 < ntiles) load_tiles(k0 + BK);
+
+        T run[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) run[i][j] = acc[i][j];
+
+        if (k0 + BK <= K) {
+            // Full chunk: products folded two at a time (one max3/min3 each).
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 2) {
+                T a0[TM], b0[TN], a1[TM], b1[TN];
+                load_frag(buf, kk, a0, b0);
+                load_frag(buf, kk + 1, a1, b1);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const T p0 = tmul<SR, T>(a0[i], b0[j]);
+                        const T p1 = tmul<SR, T>(a1[i], b1[j]);
+                        run[i][j] = tjoin<SR, T>(tjoin<SR, T>(run[i][j], p0), p1);
+                    }
+            }
+        } else {
+            // Ragged last chunk: only k < K may enter the reduction.
+            const int kcnt = int(K - k0);
+            for (int kk = 0; kk < kcnt; ++kk) {
+                T a0[TM], b0[TN];
+                load_frag(buf, kk, a0, b0);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        run[i][j] = tjoin<SR, T>(run[i][j], tmul<SR, T>(a0[i], b0[j]));
+            }
+        }
+
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                if constexpr (ARGMAX) {
+                    if (tbetter<SR, T>(run[i][j], acc[i][j])) ch[i][j] = int32_t(t);
+                }
+                acc[i][j] = run[i][j];
+            }
+
+        if (t + 1 < ntiles) store_tiles(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue ------------------------------------------------------------
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+        if (gr >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
+            if (gc < N) {
+                C[gr * N + gc] = acc[i][j];
+                if constexpr (ARGMAX) CH[gr * N + gc] = ch[i][j];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// BT[z][j][k] = B[z][k][j]   (K x N -> N x K), 32 x 32 tiles through LDS.
+// grid = (ceil(N/32), ceil(K/32), batch), block = (32, 8).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tg_transpose(const T* __restrict__ B, T* __restrict__ BT,
+                                                    int64_t K, int64_t N, int64_t sB, int64_t sBT) {
+    __shared__ T tile[32][33];
+    const int64_t z = blockIdx.z;
+    B += z * sB;
+    BT += z * sBT;
+    const int64_t n0 = int64_t(blockIdx.x) * 32;
+    const int64_t k0 = int64_t(blockIdx.y) * 32;
+    const int x = threadIdx.x, y = threadIdx.y;
+#pragma unroll
+    for (int r = y; r < 32; r += 8) {
+        const int64_t k = k0 + r, n = n0 + x;
+        if (k < K && n < N) tile[r][x] = B[k * N + n];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = y; r < 32; r += 8) {
+        const int64_t n = n0 + r, k = k0 + x;
+        if (k < K && n < N) BT[n * K + k] = tile[x][r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Exact argmax inside the winning chunk.  IDX holds the chunk (or -1) on
+// entry and the argmax on exit; C holds the final value on entry and the
+// bits of the first product equal to it on exit.  One thread per output.
+// grid = (ceil(M*N/256), 1, batch).
+// ---------------------------------------------------------------------------
+template <int SR, typename T>
+__global__ __launch_bounds__(256) void tg_resolve(const T* __restrict__ A, const T* __restrict__ BT,
+                                                  T* __restrict__ C, int32_t* __restrict__ IDX,
+                                                  int64_t M, int64_t N, int64_t K, int64_t sA,
+                                                  int64_t sBT, int64_t sC) {
+    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (o >= M * N) return;
+    const int64_t z = blockIdx.z;
+    A += z * sA;
+    BT += z * sBT;
+    C += z * sC;
+    IDX += z * sC;
+    const int32_t c = IDX[o];
+    if (c < 0) {
+        IDX[o] = 0;
+        return;
+    }
+    const int64_t i = o / N, j = o - (o / N) * N;
+    const T target = C[o];
+    const int64_t k0 = int64_t(c) * TG_CHUNK;
+    const int64_t k1 = (k0 + TG_CHUNK < K) ? k0 + TG_CHUNK : K;
+    const T* arow = A + i * K;
+    const T* brow = BT + j * K;
+    int32_t found = int32_t(k0);
+    T val = target;
+    for (int64_t k = k0; k < k1; ++k) {
+        const T p = tmul<SR, T>(arow[k], brow[k]);
+        if (p == target) {
+            found = int32_t(k);
+            val = p;
+            break;
+        }
+    }
+    IDX[o] = found;
+    C[o] = val;
+}
+
+// ---------------------------------------------------------------------------
+// Zero fill (16-byte stores + byte tail).  Used instead of hipMemsetAsync so
+// that the library records no memset nodes when a caller captures a graph.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void tg_fill_zero(unsigned char* __restrict__ p, int64_t bytes) {
+    const int64_t nvec = bytes / 16;
+    const int64_t stride = int64_t(gridDim.x) * 256;
+    for (int64_t v = int64_t(blockIdx.x) * 256 + threadIdx.x; v < nvec; v += stride)
+        reinterpret_cast<uint4*>(p)[v] = make_uint4(0u, 0u, 0u, 0u);
+    const int64_t tail0 = nvec * 16;
+    for (int64_t b = tail0 + int64_t(blockIdx.x) * 256 + threadIdx.x; b < bytes; b += stride) p[b] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// grad_A rows: one workgroup per (row i, batch z); the row of grad_A (K
+// values) is accumulated in LDS with ds_add and written out whole, so no
+// global atomics and no separate zero fill are needed.
+//   MULT=true: MaxMul rule, g *= B[kk, j]  (OTHER = B, row-major K x N).
+// grid = (M, 1, batch), block = 256, dynamic LDS = K * sizeof(T).
+// ---------------------------------------------------------------------------
+template <typename T, bool MULT>
+__global__ __launch_bounds__(256) void tg_backward_rows(const T* __restrict__ G,
+                                                        const int32_t* __restrict__ IDX,
+                                                        const T* __restrict__ OTHER,
+                                                        T* __restrict__ GA, int64_t M, int64_t N,
+                                                        int64_t K, int64_t sC, int64_t sO,
+                                                        int64_t sA) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    T* row = reinterpret_cast<T*>(lds_raw);
+    const int64_t i = blockIdx.x;
+    const int64_t z = blockIdx.z;
+    G += z * sC;
+    IDX += z * sC;
+    GA += z * sA;
+    if (MULT) OTHER += z * sO;
+    for (int64_t k = threadIdx.x; k < K; k += 256) row[k] = T(0);
+    __syncthreads();
+    for (int64_t j = threadIdx.x; j < N; j += 256) {
+        const int32_t kk = IDX[i * N + j];
+        if (kk >= 0 && int64_t(kk) < K) {
+            T g = G[i * N + j];
+            if (MULT) g = g * OTHER[int64_t(kk) * N + j];
+            atomicAdd(&row[kk], g);
+        }
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < K; k += 256) GA[i * K + k] = row[k];
+}
+
+// grad_A fallback for rows that do not fit in LDS: global atomics into a
+// zero-filled grad_A.  grid = (ceil(M*N/256), 1, batch).
+template <typename T, bool MULT>
+__global__ __launch_bounds__(256) void tg_backward_rows_global(const T* __restrict__ G,
+                                                               const int32_t* __restrict__ IDX,
+                                                               const T* __restrict__ OTHER,
+                                                               T* __restrict__ GA, int64_t M,
+                                                               int64_t N, int64_t K, int64_t sC,
+                                                               int64_t sO, int64_t sA) {
+    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (o >= M * N) return;
+    const int64_t z = blockIdx.z;
+    G += z * sC;
+    IDX += z * sC;
+    GA += z * sA;
+    if (MULT) OTHER += z * sO;
+    const int64_t i = o / N, j = o - (o / N) * N;
+    const int32_t kk = IDX[o];
+    if (kk >= 0 && int64_t(kk) < K) {
+        T g = G[o];
+        if (MULT) g = g * OTHER[int64_t(kk) * N + j];
+        unsafeAtomicAdd(&GA[i * K + kk], g);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grad_B: global atomics into a zero-filled grad_B (K x N).
+//   MULT=true: MaxMul rule, g *= A[i, kk]  (OTHER = A, row-major M x K).
+// grid = (ceil(M*N/256), 1, batch).
+// ---------------------------------------------------------------------------
+template <typename T, bool MULT>
+__global__ __launch_bounds__(256) void tg_backward_cols(const T* __restrict__ G,
+                                                        const int32_t* __restrict__ IDX,
+                                                        const T* __restrict__ OTHER,
+                                                        T* __restrict__ GB, int64_t M, int64_t N,
+                                                        int64_t K, int64_t sC, int64_t sO,
+                                                        int64_t sB) {
+    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (o >= M * N) return;
+    const int64_t z = blockIdx.z;
+    G += z * sC;
+    IDX += z * sC;
+    GB += z * sB;
+    if (MULT) OTHER += z * sO;
+    const int64_t i = o / N, j = o - (o / N) * N;
+    const int32_t kk = IDX[o];
+    if (kk >= 0 && int64_t(kk) < K) {
+        T g = G[o];
+        if (MULT) g = g * OTHER[i * K + kk];
+        unsafeAtomicAdd(&GB[int64_t(kk) * N + j], g);
+    }
+}
+
+}  // namespace tg
