@@ -151,41 +151,35 @@ int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
         int32_t* Iz = argmax ? p.IDX + z0 * p.sC : nullptr;
         dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
         if (argmax) {
-            if (vec)
-                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true>), grid, dim3(256), 0, st,
-                                   Az, Bz, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
-                                   int(tiles_n));
-            else
-                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false>), grid, dim3(256), 0, st,
-                                   Az, Bz, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
-                                   int(tiles_n));
-            TG_HIP(hipGetLastError());
-            // Resolve the exact first-k index inside each winning chunk.
-            T* BT = static_cast<T*>(ws) + 0;
+            // B^T staging for the argmax epilogue (dense, batch stride K*N).
+            T* BT = static_cast<T*>(ws);
             const int64_t sBT = p.K * p.N;
             if (p.K > 0) {
-                dim3 tg_grid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
                 if ((p.K + 31) / 32 > 65535)
                     return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
-                hipLaunchKernelGGL((tg::tg_transpose<T>), tg_grid, dim3(32, 8), 0, st, Bz, BT,
-                                   p.K, p.N, p.sB, sBT);
+                dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+                hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, Bz, BT, p.K,
+                                   p.N, p.sB, sBT);
                 TG_HIP(hipGetLastError());
             }
-            const int64_t outs = p.M * p.N;
-            const int64_t blocks = (outs + 255) / 256;
-            if (blocks > 0x7fffffffLL) return fail(TG_ERR_DIMENSION_MISMATCH, "output too large");
-            hipLaunchKernelGGL((tg::tg_resolve<SR, T>), dim3(unsigned(blocks), 1, unsigned(nb)),
-                               dim3(256), 0, st, Az, BT, Cz, Iz, p.M, p.N, p.K, p.sA, sBT, p.sC);
+            if (vec)
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true>), grid, dim3(256), 0, st,
+                                   Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
+            else
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false>), grid, dim3(256), 0, st,
+                                   Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
             TG_HIP(hipGetLastError());
         } else {
             if (vec)
                 hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, false, true>), grid, dim3(256), 0, st,
-                                   Az, Bz, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                    int(tiles_m), int(tiles_n));
             else
                 hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, false, false>), grid, dim3(256), 0,
-                                   st, Az, Bz, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
-                                   int(tiles_m), int(tiles_n));
+                                   st, Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB,
+                                   p.sC, int(tiles_m), int(tiles_n));
             TG_HIP(hipGetLastError());
         }
     }

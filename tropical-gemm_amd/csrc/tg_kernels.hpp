@@ -4,8 +4,7 @@
 //   tg_gemm_tiles      value-only and argmax GEMM for every dtype/semiring
 //                      (TROPICAL_GEMM_{F32,F64,I32,I64} 86-520,
 //                       TROPICAL_GEMM_ARGMAX_* 526-996, batched 1094-1219)
-//   tg_transpose       B -> B^T staging for the argmax resolve step (new)
-//   tg_resolve         exact first-k argmax inside the winning chunk (new)
+//   tg_transpose       B -> B^T staging for the argmax epilogue (new)
 //   tg_backward_rows   grad_A scatter (TROPICAL_BACKWARD_A 1002-1018)
 //   tg_backward_cols   grad_B scatter (TROPICAL_BACKWARD_B 1020-1036)
 //   tg_fill_zero       zero fill used instead of hipMemsetAsync
@@ -15,18 +14,18 @@
 // (kernels.rs:370-430 does the same trick in the other direction).
 //
 // Argmax scheme ("chunked argmax").  K is cut into chunks of TG_CHUNK = 32
-// consecutive k (one LDS k-tile).  Inside a chunk each output folds products
-// with max/min only (two products per v_max3/v_min3).  At the chunk end one
-// compare against the value held before the chunk records the chunk index if
-// the chunk strictly improved it.  Because max/min select an operand exactly
-// and earlier chunks only lose on strict improvement, the first k attaining
-// the final value lies in the recorded chunk; tg_resolve finds it by
-// recomputing that chunk's <= 32 products (reading A and B^T rows) and takes
-// the first k whose product equals the final value, writing both the index
-// and that product's bits (so a -0/+0 tie keeps the first occurrence's sign,
-// exactly like the CPU select rule).  The per-(i,j,k) VALU cost is one
-// (x), half a max3 and 2/32 for the bookkeeping instead of the four
-// operations of a per-k compare-and-select.
+// consecutive k (one LDS k-tile).  Inside a chunk each output folds its
+// products into a chunk maximum with max/min only (two products per
+// v_max3/v_min3).  At the chunk end one compare against the running value
+// records the chunk index if the chunk strictly improved it.  Because max/min
+// select an operand exactly and earlier chunks only lose on strict
+// improvement, the first k attaining the final value lies in the recorded
+// chunk; the kernel's epilogue finds it by recomputing that chunk's <= 32
+// products (reading A and B^T rows) and takes the first k whose product
+// equals the final value, writing both the index and that product's bits (so
+// a -0/+0 tie keeps the first occurrence's sign, exactly like the CPU select
+// rule).  The per-(i,j,k) VALU cost is one (x), half a max3 and 3/32 for the
+// bookkeeping instead of the four operations of a per-k compare-and-select.
 #pragma once
 
 #include "tg_device.hpp"
@@ -86,16 +85,22 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 // ---------------------------------------------------------------------------
 // Main GEMM kernel.
 //   ARGMAX=false : C = A (x) B.
-//   ARGMAX=true  : C = A (x) B and CH = winning chunk (or -1 when the tropical
-//                  zero was never beaten); tg_resolve turns CH into argmax.
-//   VEC          : K and N are multiples of 16/sizeof(T) and A, B are 16-byte
-//                  aligned, so tiles load with 16-byte global loads.
+//   ARGMAX=true  : C = A (x) B and IDX = the first k attaining C.  The main
+//                  loop folds each chunk of TG_CHUNK consecutive k into a
+//                  chunk maximum cm and records the chunk when cm strictly
+//                  beats the running value; the epilogue then re-reads that
+//                  chunk's A-row and B^T-row segments (BT from tg_transpose)
+//                  and takes the first k whose product equals the final value.
+//   VEC          : K and N are multiples of 16/sizeof(T) and A, B, BT are
+//                  16-byte aligned, so tiles and argmax windows use 16-byte
+//                  global loads.
 // grid = (tiles_m * tiles_n, 1, batch), block = 256.
 // ---------------------------------------------------------------------------
 template <int SR, typename T, bool ARGMAX, bool VEC>
 __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
-    const T* __restrict__ A, const T* __restrict__ B, T* __restrict__ C, int32_t* __restrict__ CH,
-    int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC, int tiles_m, int tiles_n) {
+    const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
+    T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
+    int64_t sB, int64_t sC, int tiles_m, int tiles_n) {
     using Cfg = TileCfg<T>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, TM = Cfg::TM, TN = Cfg::TN, BK = TG_CHUNK;
     constexpr int VW = Vec16<T>::N;          // elements per 16-byte vector
@@ -119,7 +124,10 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     A += z * sA;
     B += z * sB;
     C += z * sC;
-    if (ARGMAX) CH += z * sC;
+    if (ARGMAX) {
+        IDX += z * sC;
+        BT += z * (N * K);
+    }
 
     // ---- global -> register staging ------------------------------------
     Vec16<T> ra[NVA], rb[NVB];
@@ -184,6 +192,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     };
 
     // ---- accumulators ------------------------------------------------------
+    // acc: running value; ch: last chunk that strictly improved it (-1: none,
+    // i.e. the tropical zero was never beaten).
     T acc[TM][TN];
     int32_t ch[TM][TN];
 #pragma unroll
@@ -219,17 +229,20 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         const int64_t k0 = t * BK;
         if (t + 1 < ntiles) load_tiles(k0 + BK);
 
-        T run[TM][TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) run[i][j] = acc[i][j];
-
+        // Chunk maximum (minimum for MinPlus) over this chunk's products.
+        T cm[TM][TN];
         if (k0 + BK <= K) {
-            // Full chunk: products folded two at a time (one max3/min3 each).
+            T a0[TM], b0[TN], a1[TM], b1[TN];
+            load_frag(buf, 0, a0, b0);
+            load_frag(buf, 1, a1, b1);
 #pragma unroll
-            for (int kk = 0; kk < BK; kk += 2) {
-                T a0[TM], b0[TN], a1[TM], b1[TN];
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a0[i], b0[j]), tmul<SR, T>(a1[i], b1[j]));
+            // Remaining products two at a time: one max3/min3 per pair.
+#pragma unroll
+            for (int kk = 2; kk < BK; kk += 2) {
                 load_frag(buf, kk, a0, b0);
                 load_frag(buf, kk + 1, a1, b1);
 #pragma unroll
@@ -238,31 +251,38 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                     for (int j = 0; j < TN; ++j) {
                         const T p0 = tmul<SR, T>(a0[i], b0[j]);
                         const T p1 = tmul<SR, T>(a1[i], b1[j]);
-                        run[i][j] = tjoin<SR, T>(tjoin<SR, T>(run[i][j], p0), p1);
+                        cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
                     }
             }
         } else {
             // Ragged last chunk: only k < K may enter the reduction.
             const int kcnt = int(K - k0);
-            for (int kk = 0; kk < kcnt; ++kk) {
-                T a0[TM], b0[TN];
+            T a0[TM], b0[TN];
+            load_frag(buf, 0, a0, b0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) cm[i][j] = tmul<SR, T>(a0[i], b0[j]);
+            for (int kk = 1; kk < kcnt; ++kk) {
                 load_frag(buf, kk, a0, b0);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        run[i][j] = tjoin<SR, T>(run[i][j], tmul<SR, T>(a0[i], b0[j]));
+                        cm[i][j] = tjoin<SR, T>(cm[i][j], tmul<SR, T>(a0[i], b0[j]));
             }
         }
 
+        // Strict improvement only: an equal chunk maximum keeps the earlier
+        // chunk, which is the reference's "keep acc iff acc >= p" rule.
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 if constexpr (ARGMAX) {
-                    if (tbetter<SR, T>(run[i][j], acc[i][j])) ch[i][j] = int32_t(t);
+                    if (tbetter<SR, T>(cm[i][j], acc[i][j])) ch[i][j] = int32_t(t);
                 }
-                acc[i][j] = run[i][j];
+                acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
             }
 
         if (t + 1 < ntiles) store_tiles(buf ^ 1);
@@ -270,16 +290,87 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     }
 
     // ---- epilogue ------------------------------------------------------------
+    if constexpr (!ARGMAX) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-        const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
-        if (gr >= M) continue;
+        for (int i = 0; i < TM; ++i) {
+            const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+            if (gr >= M) continue;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
-            if (gc < N) {
-                C[gr * N + gc] = acc[i][j];
-                if constexpr (ARGMAX) CH[gr * N + gc] = ch[i][j];
+            for (int j = 0; j < TN; ++j) {
+                const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
+                if (gc < N) C[gr * N + gc] = acc[i][j];
+            }
+        }
+    } else {
+        // Exact argmax inside the recorded chunk.  Products in the chunk
+        // before it never equal the final value (that chunk would not have
+        // been beaten strictly), so a 16-byte-aligned window of TG_CHUNK
+        // products ending at K may be searched for the ragged last chunk.
+        // The value written is the bits of the first equal product, so a
+        // -0/+0 tie keeps the first occurrence's sign like the CPU rule.
+        constexpr int NW = BK / VW;  // 16-byte vectors per window
+        const bool vec_windows = VEC && K >= BK;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+            const int64_t grl = gr < M ? gr : M - 1;  // clamped row for loads
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
+                const int64_t gcl = gc < N ? gc : N - 1;
+                const T target = acc[i][j];
+                T val = target;
+                int32_t idx = 0;
+                if (vec_windows) {
+                    const int64_t c = ch[i][j] < 0 ? 0 : ch[i][j];
+                    const int64_t ws = (c * BK < K - BK) ? c * BK : K - BK;
+                    const T* ap = A + grl * K + ws;
+                    const T* bp = BT + gcl * K + ws;
+                    Vec16<T> av[NW], bv[NW];
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) {
+                        av[w] = reinterpret_cast<const Vec16<T>*>(ap)[w];
+                        bv[w] = reinterpret_cast<const Vec16<T>*>(bp)[w];
+                    }
+                    // Last match scanning downwards == first match.  Groups of
+                    // 8 compares keep few lane masks live at once.
+                    int32_t f = 0;
+#pragma unroll
+                    for (int g = BK / 8 - 1; g >= 0; --g) {
+#pragma unroll
+                        for (int kk = g * 8 + 7; kk >= g * 8; --kk) {
+                            const T p = tmul<SR, T>(av[kk / VW].v[kk % VW], bv[kk / VW].v[kk % VW]);
+                            f = (p == target) ? kk : f;
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    idx = int32_t(ws + f);
+                    if constexpr (std::is_floating_point<T>::value) {
+                        // Equal values have equal bits except +0/-0: take the
+                        // sign of the first zero product (rare branch).
+                        if (target == T(0)) val = tmul<SR, T>(ap[f], bp[f]);
+                    }
+                } else if (gr < M && gc < N && ch[i][j] >= 0) {
+                    const int64_t k0 = int64_t(ch[i][j]) * BK;
+                    const int64_t k1 = (k0 + BK < K) ? k0 + BK : K;
+                    idx = int32_t(k0);
+                    for (int64_t k = k0; k < k1; ++k) {
+                        const T p = tmul<SR, T>(A[gr * K + k], BT[gc * K + k]);
+                        if (p == target) {
+                            idx = int32_t(k);
+                            val = p;
+                            break;
+                        }
+                    }
+                }
+                if (ch[i][j] < 0) {  // the tropical zero was never beaten
+                    val = tzero<SR, T>();
+                    idx = 0;
+                }
+                if (gr < M && gc < N) {
+                    C[gr * N + gc] = val;
+                    IDX[gr * N + gc] = idx;
+                }
             }
         }
     }
@@ -310,49 +401,6 @@ __global__ __launch_bounds__(256) void tg_transpose(const T* __restrict__ B, T* 
         const int64_t n = n0 + r, k = k0 + x;
         if (k < K && n < N) BT[n * K + k] = tile[x][r];
     }
-}
-
-// ---------------------------------------------------------------------------
-// Exact argmax inside the winning chunk.  IDX holds the chunk (or -1) on
-// entry and the argmax on exit; C holds the final value on entry and the
-// bits of the first product equal to it on exit.  One thread per output.
-// grid = (ceil(M*N/256), 1, batch).
-// ---------------------------------------------------------------------------
-template <int SR, typename T>
-__global__ __launch_bounds__(256) void tg_resolve(const T* __restrict__ A, const T* __restrict__ BT,
-                                                  T* __restrict__ C, int32_t* __restrict__ IDX,
-                                                  int64_t M, int64_t N, int64_t K, int64_t sA,
-                                                  int64_t sBT, int64_t sC) {
-    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (o >= M * N) return;
-    const int64_t z = blockIdx.z;
-    A += z * sA;
-    BT += z * sBT;
-    C += z * sC;
-    IDX += z * sC;
-    const int32_t c = IDX[o];
-    if (c < 0) {
-        IDX[o] = 0;
-        return;
-    }
-    const int64_t i = o / N, j = o - (o / N) * N;
-    const T target = C[o];
-    const int64_t k0 = int64_t(c) * TG_CHUNK;
-    const int64_t k1 = (k0 + TG_CHUNK < K) ? k0 + TG_CHUNK : K;
-    const T* arow = A + i * K;
-    const T* brow = BT + j * K;
-    int32_t found = int32_t(k0);
-    T val = target;
-    for (int64_t k = k0; k < k1; ++k) {
-        const T p = tmul<SR, T>(arow[k], brow[k]);
-        if (p == target) {
-            found = int32_t(k);
-            val = p;
-            break;
-        }
-    }
-    IDX[o] = found;
-    C[o] = val;
 }
 
 // ---------------------------------------------------------------------------
