@@ -290,3 +290,88 @@ def test_context_and_memory_entry_points():
     nat.check(lib.tg_memcpy_dtoh(0, back.ctypes.data_as(ctypes.c_void_p), ptr, host.nbytes))
     assert np.all(back[:25] == 0) and np.array_equal(back[25:], host[25:])
     nat.check(lib.tg_free(0, ptr))
+
+
+# ---------------------------------------------------------------------------
+# Full-tile shapes: 32-bit problems with M % 64 == 0, N % 128 == 0 and
+# K % 32 == 0 take the direct-to-LDS kernel; these pin it to the oracle.
+# ---------------------------------------------------------------------------
+
+ALIGNED_SHAPES = [(64, 32, 128), (128, 160, 256), (320, 1024, 384), (64, 4096, 128)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_full_tile_shapes(sr, dt):
+    rng = np.random.default_rng(300 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in ALIGNED_SHAPES:
+        print(f"[case] full-tile {sr} {dt} m={m} k={k} n={n}", flush=True)
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        c_ref, am_ref = oracle.gemm(sr, a, b)
+        c, am = gpu_gemm(sr, a, b, True)
+        assert_exact(c, am, c_ref, am_ref)
+        c, _ = gpu_gemm(sr, a, b, False)
+        assert_exact(c, None, c_ref, None)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+def test_full_tile_heavy_ties(sr, dt):
+    rng = np.random.default_rng(78)
+    dtype = tc.NP_DTYPES[dt]
+    a = rng.integers(0, 3, size=(128, 320)).astype(dtype)
+    b = rng.integers(0, 3, size=(320, 256)).astype(dtype)
+    c, am = gpu_gemm(sr, a, b)
+    assert_exact(c, am, *oracle.gemm(sr, a, b))
+
+
+def test_full_tile_special_values():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((128, 256)).astype(np.float32)
+    b = rng.standard_normal((256, 256)).astype(np.float32)
+    a[rng.random(a.shape) < 0.3] = np.inf
+    b[rng.random(b.shape) < 0.3] = np.inf
+    assert_exact(*gpu_gemm("minplus", a, b), *oracle.gemm("minplus", a, b))
+    a2 = np.where(np.isinf(a), -np.inf, a).astype(np.float32)
+    b2 = np.where(np.isinf(b), -np.inf, b).astype(np.float32)
+    a2[5, :] = -np.inf
+    c, am = gpu_gemm("maxplus", a2, b2)
+    assert_exact(c, am, *oracle.gemm("maxplus", a2, b2))
+    assert np.all(np.isneginf(c[5])) and np.all(am[5] == 0)
+    a3 = rng.integers(-2, 3, size=(64, 96)).astype(np.float32)
+    b3 = rng.integers(-2, 3, size=(96, 128)).astype(np.float32)
+    assert_exact(*gpu_gemm("maxmul", a3, b3), *oracle.gemm("maxmul", a3, b3))
+    # signed zeros: -0 at k=0 ties +0 later; the first occurrence wins
+    z = np.zeros((64, 64), np.float32)
+    z[:, 0] = -0.0
+    bz = np.full((64, 128), -1.0, np.float32)
+    bz[0, :] = -0.0
+    bz[40, :] = 0.0
+    c, am = gpu_gemm("maxplus", z, bz)
+    assert_exact(c, am, *oracle.gemm("maxplus", z, bz))
+    assert np.all(np.signbit(c)) and np.all(am == 0)
+
+
+def test_full_tile_strided_batched():
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    rng = np.random.default_rng(13)
+    batch, m, k, n = 3, 64, 96, 128
+    sa, sb, sc = m * k + 4, k * n + 8, m * n + 12
+    a = rng.standard_normal(batch * sa).astype(np.float32)
+    b = rng.standard_normal(batch * sb).astype(np.float32)
+    ta, tb = _dev(a), _dev(b)
+    c = torch.zeros(batch * sc, dtype=torch.float32, device=DEV)
+    am = torch.zeros(batch * sc, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm_strided_batched(0, nat.SEMIRING["maxplus"], 0, 0, _p(ta), _p(tb), _p(c),
+                                          _p(am), batch, m, n, k, sa, sb, sc, None))
+    torch.cuda.synchronize()
+    c_np, am_np = c.cpu().numpy(), am.cpu().numpy()
+    for t in range(batch):
+        at = a[t * sa: t * sa + m * k].reshape(m, k)
+        bt = b[t * sb: t * sb + k * n].reshape(k, n)
+        assert_exact(c_np[t * sc: t * sc + m * n].reshape(m, n),
+                     am_np[t * sc: t * sc + m * n].reshape(m, n), *oracle.gemm("maxplus", at, bt))

@@ -13,6 +13,7 @@
 #include <string>
 
 #include "../../include/tropical_gemm_hip.h"
+#include "tg_gemm_dl.hpp"
 #include "tg_kernels.hpp"
 
 namespace {
@@ -128,8 +129,50 @@ struct Problem {
     int64_t batch, M, N, K, sA, sB, sC;
 };
 
+// Direct-to-LDS kernel for 32-bit types when every tile is full.
+template <int SR, typename T>
+int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
+    using Cfg = tg::DlCfg;
+    const int64_t tiles_m = p.M / Cfg::BM;
+    const int64_t tiles_n = p.N / Cfg::BN;
+    if (tiles_m * tiles_n > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    const T* A = static_cast<const T*>(p.A);
+    const T* B = static_cast<const T*>(p.B);
+    T* C = static_cast<T*>(p.C);
+    const bool argmax = p.IDX != nullptr;
+    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+        const T* Az = A + z0 * p.sA;
+        const T* Bz = B + z0 * p.sB;
+        T* Cz = C + z0 * p.sC;
+        dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+        if (argmax) {
+            T* BT = static_cast<T*>(ws);
+            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+            if ((p.K + 31) / 32 > 65535)
+                return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
+            hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, Bz, BT, p.K, p.N,
+                               p.sB, p.K * p.N);
+            TG_HIP(hipGetLastError());
+            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true>), grid, dim3(256), Cfg::LDS_BYTES, st,
+                               Az, Bz, BT, Cz, p.IDX + z0 * p.sC, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                               int(tiles_m), int(tiles_n));
+        } else {
+            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false>), grid, dim3(256), Cfg::LDS_BYTES, st,
+                               Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                               int(tiles_m), int(tiles_n));
+        }
+        TG_HIP(hipGetLastError());
+    }
+    return TG_OK;
+}
+
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
+    if constexpr (sizeof(T) == 4) {
+        if (tg::dl_fits(p.M, p.N, p.K, p.sA, p.sB, p.A, p.B)) return run_gemm_dl<SR, T>(p, ws, st);
+    }
     using Cfg = tg::TileCfg<T>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;

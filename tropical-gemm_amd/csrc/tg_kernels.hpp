@@ -308,68 +308,95 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         // products ending at K may be searched for the ragged last chunk.
         // The value written is the bits of the first equal product, so a
         // -0/+0 tie keeps the first occurrence's sign like the CPU rule.
-        constexpr int NW = BK / VW;  // 16-byte vectors per window
+        constexpr int NW = BK / VW;                // 16-byte vectors per window
+        constexpr int G = sizeof(T) == 4 ? 2 : 1;  // outputs with windows in flight
         const bool vec_windows = VEC && K >= BK;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
             const int64_t grl = gr < M ? gr : M - 1;  // clamped row for loads
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
-                const int64_t gcl = gc < N ? gc : N - 1;
-                const T target = acc[i][j];
-                T val = target;
-                int32_t idx = 0;
+            for (int j0 = 0; j0 < TN; j0 += G) {
+                T val[G];
+                int32_t idx[G];
+                int64_t gc[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    gc[g] = col0 + ((j0 + g) / 4) * 64 + tx * 4 + ((j0 + g) % 4);
+                    val[g] = acc[i][j0 + g];
+                    idx[g] = 0;
+                }
                 if (vec_windows) {
-                    const int64_t c = ch[i][j] < 0 ? 0 : ch[i][j];
-                    const int64_t ws = (c * BK < K - BK) ? c * BK : K - BK;
-                    const T* ap = A + grl * K + ws;
-                    const T* bp = BT + gcl * K + ws;
-                    Vec16<T> av[NW], bv[NW];
+                    Vec16<T> av[G][NW], bv[G][NW];
+                    const T* ap[G];
+                    const T* bp[G];
+                    int64_t ws[G];
 #pragma unroll
-                    for (int w = 0; w < NW; ++w) {
-                        av[w] = reinterpret_cast<const Vec16<T>*>(ap)[w];
-                        bv[w] = reinterpret_cast<const Vec16<T>*>(bp)[w];
-                    }
-                    // Last match scanning downwards == first match.  Groups of
-                    // 8 compares keep few lane masks live at once.
-                    int32_t f = 0;
+                    for (int g = 0; g < G; ++g) {
+                        const int64_t gcl = gc[g] < N ? gc[g] : N - 1;
+                        const int64_t c = ch[i][j0 + g] < 0 ? 0 : ch[i][j0 + g];
+                        ws[g] = (c * BK < K - BK) ? c * BK : K - BK;
+                        ap[g] = A + grl * K + ws[g];
+                        bp[g] = BT + gcl * K + ws[g];
 #pragma unroll
-                    for (int g = BK / 8 - 1; g >= 0; --g) {
-#pragma unroll
-                        for (int kk = g * 8 + 7; kk >= g * 8; --kk) {
-                            const T p = tmul<SR, T>(av[kk / VW].v[kk % VW], bv[kk / VW].v[kk % VW]);
-                            f = (p == target) ? kk : f;
+                        for (int w = 0; w < NW; ++w) {
+                            av[g][w] = reinterpret_cast<const Vec16<T>*>(ap[g])[w];
+                            bv[g][w] = reinterpret_cast<const Vec16<T>*>(bp[g])[w];
                         }
-                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    idx = int32_t(ws + f);
-                    if constexpr (std::is_floating_point<T>::value) {
-                        // Equal values have equal bits except +0/-0: take the
-                        // sign of the first zero product (rare branch).
-                        if (target == T(0)) val = tmul<SR, T>(ap[f], bp[f]);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const T target = val[g];
+                        // Last match scanning downwards == first match.  Groups
+                        // of 8 compares keep few lane masks live at once.
+                        int32_t f = 0;
+#pragma unroll
+                        for (int q = BK / 8 - 1; q >= 0; --q) {
+#pragma unroll
+                            for (int kk = q * 8 + 7; kk >= q * 8; --kk) {
+                                const T p = tmul<SR, T>(av[g][kk / VW].v[kk % VW],
+                                                        bv[g][kk / VW].v[kk % VW]);
+                                f = (p == target) ? kk : f;
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        idx[g] = int32_t(ws[g] + f);
+                        if constexpr (std::is_floating_point<T>::value) {
+                            // Equal values have equal bits except +0/-0: take
+                            // the sign of the first zero product (rare branch).
+                            if (target == T(0)) val[g] = tmul<SR, T>(ap[g][f], bp[g][f]);
+                        }
                     }
-                } else if (gr < M && gc < N && ch[i][j] >= 0) {
-                    const int64_t k0 = int64_t(ch[i][j]) * BK;
-                    const int64_t k1 = (k0 + BK < K) ? k0 + BK : K;
-                    idx = int32_t(k0);
-                    for (int64_t k = k0; k < k1; ++k) {
-                        const T p = tmul<SR, T>(A[gr * K + k], BT[gc * K + k]);
-                        if (p == target) {
-                            idx = int32_t(k);
-                            val = p;
-                            break;
+                } else {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const int32_t c = ch[i][j0 + g];
+                        if (gr < M && gc[g] < N && c >= 0) {
+                            const T target = val[g];
+                            const int64_t k0 = int64_t(c) * BK;
+                            const int64_t k1 = (k0 + BK < K) ? k0 + BK : K;
+                            idx[g] = int32_t(k0);
+                            for (int64_t k = k0; k < k1; ++k) {
+                                const T p = tmul<SR, T>(A[gr * K + k], BT[gc[g] * K + k]);
+                                if (p == target) {
+                                    idx[g] = int32_t(k);
+                                    val[g] = p;
+                                    break;
+                                }
+                            }
                         }
                     }
                 }
-                if (ch[i][j] < 0) {  // the tropical zero was never beaten
-                    val = tzero<SR, T>();
-                    idx = 0;
-                }
-                if (gr < M && gc < N) {
-                    C[gr * N + gc] = val;
-                    IDX[gr * N + gc] = idx;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if (ch[i][j0 + g] < 0) {  // the tropical zero was never beaten
+                        val[g] = tzero<SR, T>();
+                        idx[g] = 0;
+                    }
+                    if (gr < M && gc[g] < N) {
+                        C[gr * N + gc[g]] = val[g];
+                        IDX[gr * N + gc[g]] = idx[g];
+                    }
                 }
             }
         }
