@@ -4,11 +4,13 @@
 
 A step is one call of the C ABI entry point ``tg_gemm_ws`` on the config's
 synthetic inputs (already resident in HBM): for argmax configs that is the
-B^T staging kernel, the tiled GEMM kernel and the argmax resolve kernel.
-Steps are timed with HIP events on the stream the kernels run on (torch's
-current stream), bracketed by device synchronisation.  ``value`` is tropical
-GOP/s = 2*M*N*K / t_step, the reference's own "GFLOPS-equivalent" count
-(crates/tropical-gemm/examples/bench_rust.rs:121).
+B^T staging kernel and the tiled GEMM kernel (whose epilogue resolves the
+argmax).  Steps are timed with HIP events on the stream the kernels run on
+(torch's current stream), bracketed by device synchronisation.  ``value`` is
+tropical GOP/s = 2*M*N*K / t_step, the reference's own "GFLOPS-equivalent"
+count (crates/tropical-gemm/examples/bench_rust.rs:121).  ``roofline`` is
+for the GEMM kernel alone, timed by the library's event hook
+(tg_kernel_timing_*) on the same stream.
 
 The CPU baseline is the single-thread restatement of the reference's CPU
 argmax path (oracle/tg_oracle.c, ``tgo_portable_argmax_f32``) timed on a row
@@ -32,13 +34,30 @@ sys.path.insert(0, os.path.join(ROOT, "tropical-gemm_amd"))
 
 METRIC = ("tropical GOP/s (2·M·N·K) MaxPlus f32 4096³ +argmax, 1 GPU; "
           "% VALU peak")
-PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector peak
-HBM_PEAK_GBS = 8000.0         # MI355X published HBM3E bandwidth
-# Tropical VALU ceiling for f32 without packed FP32 ops: one v_add_f32 per
-# (i,j,k) plus half a v_max3_f32 -> 1.5 issue slots for 2 ops; 256 CU x 64
-# lanes x 2.4 GHz = 39.32e12 slots/s  ->  52.4e12 ops/s.
-TROP_CEILING_TOPS = 39.32 * 2 / 1.5
+PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector (and dense) peak
+# Tropical roofline: (x) and (+) are one VALU op each with no fused form; the
+# densest mix (v_add_f32 + half a v_max3_f32) issues 2 tropical ops per 4
+# wave64-cycles per lane, i.e. half the FMA peak: 78.6e12 ops/s at 2.4 GHz.
+TROP_PEAK_TOPS = PEAK_FP32_TFLOPS / 2
 DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
+WORKLOAD_NAMES = {
+    "P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
+    "C1": "C1: MaxPlus f32 1024^3 +argmax",
+    "C2": "C2: MinPlus f32 4096^3 +argmax, 10% +inf, zero diagonal",
+    "C3": "C3: MaxMul f32 8192x2048x4096 value-only",
+    "C4": "C4: MaxPlus i32 262144x128x128 +argmax",
+}
+KERNEL_NAMES = {
+    "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
+    "C1": "tg_gemm_dl<MaxPlus, f32, argmax>",
+    "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
+    "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
+    "C4": "tg_gemm_dl<MaxPlus, i32, argmax>",
+}
+# HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
+# and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
+# (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md).  Configs not profiled: None.
+TRAFFIC = {"P": 2.746e9}
 
 
 def cpu_model() -> str:
@@ -82,8 +101,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4"])
-    ap.add_argument("--cpu-rows", type=int, default=768,
+    ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="after timing, copy this many MiB once (a known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -125,6 +147,7 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
+    # Step timing: events on the stream every kernel of the step runs on.
     t0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(args.steps):
@@ -133,6 +156,21 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     wall = time.perf_counter() - t0
     ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    # Dominant-kernel timing: the library records a HIP event pair on the same
+    # stream around its main GEMM kernel (B^T staging excluded).  Separate
+    # pass over the same number of steps, so the step timing above carries no
+    # event overhead.
+    tot = ctypes.c_double(0.0)
+    nl = ctypes.c_int64(0)
+    nat.check(lib.tg_kernel_timing_read(ctypes.byref(tot), ctypes.byref(nl)))  # clear
+    nat.check(lib.tg_kernel_timing_enable(1))
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize(dev)
+    nat.check(lib.tg_kernel_timing_enable(0))
+    nat.check(lib.tg_kernel_timing_read(ctypes.byref(tot), ctypes.byref(nl)))
+    ms_kernel = tot.value / max(nl.value, 1)
 
     # Post-timing sanity check (outside the timed region): every output equals
     # the product at its argmax, bit-exactly.
@@ -146,7 +184,7 @@ def main() -> int:
 
     ops = 2.0 * m * n * k
     gops = ops / (ms_step / 1e3) / 1e9
-    achieved_tops = gops / 1e3
+    kernel_tops = ops / (ms_kernel / 1e3) / 1e12
     esize = a.element_size()
     algo_bytes = esize * (m * k + k * n + m * n) + (4 * m * n if am is not None else 0)
     out = {
@@ -162,31 +200,38 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": DTYPE_NAME[cfg["dtype"]],
         "data": "synthetic (seeded torch Philox on device; workloads.py)",
-        "config": {"workload": {"P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
-                                "C1": "C1: MaxPlus f32 1024^3 +argmax",
-                                "C2": "C2: MinPlus f32 4096^3 +argmax, 10% +inf, zero diagonal",
-                                "C3": "C3: MaxMul f32 8192x2048x4096 value-only",
-                                "C4": "C4: MaxPlus i32 262144x128x128 +argmax"}[args.config],
+        "config": {"workload": WORKLOAD_NAMES[args.config],
                    "semiring": cfg["semiring"], "m": m, "n": n, "k": k,
                    "argmax": cfg["argmax"], "layout": "row-major", "parallelism": "none (1 GPU)"},
         "roofline": {
+            # Tropical (+)/(x) has no MFMA form: the kernel is bound by the
+            # vector ALU.  peak = MI355X published FP32 vector/dense peak.
             "bound": "valu",
-            "achieved": round(achieved_tops, 3),
+            "achieved": round(kernel_tops, 3),
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(achieved_tops / PEAK_FP32_TFLOPS, 4),
-            "traffic": None,
+            "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4),
+            "traffic": TRAFFIC.get(args.config),
+            "kernel": KERNEL_NAMES[args.config],
+            "kernel_ms": round(ms_kernel, 4),
+            "kernel_launches_timed": int(nl.value),
             "ops_per_launch": ops,
-            "timed": "tg_gemm_ws step (B^T staging + tile GEMM + argmax resolve)",
-            "trop_valu_ceiling": round(TROP_CEILING_TOPS, 1),
-            "frac_of_trop_valu_ceiling": round(achieved_tops / TROP_CEILING_TOPS, 4),
+            "trop_peak": TROP_PEAK_TOPS,
+            "frac_of_trop_peak": round(kernel_tops / TROP_PEAK_TOPS, 4),
             "algorithmic_bytes": algo_bytes,
-            "algorithmic_GBps": round(algo_bytes / (ms_step / 1e3) / 1e9, 1),
         },
+        "step_frac_of_trop_peak": round(gops / 1e3 / TROP_PEAK_TOPS, 4),
         "wall_s_timed_region": round(wall, 4),
         "argmax_consistency_check": check,
         "device": torch.cuda.get_device_name(dev),
     }
+    if args.copy_mib > 0:
+        src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize(dev)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        out["copy_calibration_bytes"] = args.copy_mib << 20
     if args.cpu_rows > 0 and args.config == "P":
         out["cpu_baseline"] = run_cpu_baseline(args.cpu_rows)
         out["gpu_vs_cpu_baseline"] = round(gops / out["cpu_baseline"]["value"], 1)

@@ -87,6 +87,18 @@ int tg_memset_zero(int device, void* ptr, size_t bytes, void* stream);
 int tg_synchronize(int device);
 int tg_stream_synchronize(int device, void* stream);
 
+/* ---- kernel timing (diagnostics) ----------------------------------------
+ * No counterpart in the reference; used by benchmarks to time the main GEMM
+ * kernel apart from the B^T staging kernel that argmax calls also launch. */
+
+/* on != 0: every forward call records a HIP event pair on its stream around
+ * its main GEMM kernel(s).  Off by default (no events, no overhead). */
+int tg_kernel_timing_enable(int on);
+/* Waits for the recorded events, returns the summed main-kernel time in
+ * milliseconds and the number of launches since the last read, and clears
+ * the record. */
+int tg_kernel_timing_read(double* total_ms, int64_t* launches);
+
 /* ---- forward ----------------------------------------------------------- */
 
 /*

@@ -11,6 +11,8 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/tropical_gemm_hip.h"
 #include "tg_gemm_dl.hpp"
@@ -99,6 +101,48 @@ int select_device(int device) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Optional event timing of the main GEMM kernels (tg_kernel_timing_*).
+std::atomic<bool> g_timing{false};
+std::mutex g_timing_mu;
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_timing_events;
+
+// Records an event pair around the launches made during its lifetime when
+// timing is enabled; does nothing otherwise.
+class KernelTimer {
+  public:
+    explicit KernelTimer(hipStream_t st) : st_(st) {
+        if (!g_timing.load(std::memory_order_relaxed)) return;
+        if (hipEventCreate(&e0_) != hipSuccess || hipEventCreate(&e1_) != hipSuccess ||
+            hipEventRecord(e0_, st_) != hipSuccess) {
+            release();
+            return;
+        }
+        on_ = true;
+    }
+    ~KernelTimer() {
+        if (!on_) return;
+        if (hipEventRecord(e1_, st_) != hipSuccess) {
+            release();
+            return;
+        }
+        std::lock_guard<std::mutex> lk(g_timing_mu);
+        g_timing_events.emplace_back(e0_, e1_);
+    }
+    KernelTimer(const KernelTimer&) = delete;
+    KernelTimer& operator=(const KernelTimer&) = delete;
+
+  private:
+    void release() {
+        if (e0_) (void)hipEventDestroy(e0_);
+        if (e1_) (void)hipEventDestroy(e1_);
+        e0_ = e1_ = nullptr;
+        on_ = false;
+    }
+    hipStream_t st_;
+    hipEvent_t e0_ = nullptr, e1_ = nullptr;
+    bool on_ = false;
+};
+
 // ----------------------------------------------------------------------------
 // Launch helpers
 // ----------------------------------------------------------------------------
@@ -155,10 +199,12 @@ int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
             hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, Bz, BT, p.K, p.N,
                                p.sB, p.K * p.N);
             TG_HIP(hipGetLastError());
+            KernelTimer timer(st);
             hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true>), grid, dim3(256), Cfg::LDS_BYTES, st,
                                Az, Bz, BT, Cz, p.IDX + z0 * p.sC, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                int(tiles_m), int(tiles_n));
         } else {
+            KernelTimer timer(st);
             hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false>), grid, dim3(256), Cfg::LDS_BYTES, st,
                                Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                int(tiles_m), int(tiles_n));
@@ -205,6 +251,7 @@ int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
                                    p.N, p.sB, sBT);
                 TG_HIP(hipGetLastError());
             }
+            KernelTimer timer(st);
             if (vec)
                 hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true>), grid, dim3(256), 0, st,
                                    Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
@@ -215,6 +262,7 @@ int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
                                    int(tiles_m), int(tiles_n));
             TG_HIP(hipGetLastError());
         } else {
+            KernelTimer timer(st);
             if (vec)
                 hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, false, true>), grid, dim3(256), 0, st,
                                    Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
@@ -575,6 +623,35 @@ int tg_stream_synchronize(int device, void* stream) {
     if (rc != TG_OK) return rc;
     TG_HIP(hipStreamSynchronize(as_stream(stream)));
     return TG_OK;
+}
+
+int tg_kernel_timing_enable(int on) {
+    g_timing.store(on != 0);
+    return TG_OK;
+}
+
+int tg_kernel_timing_read(double* total_ms, int64_t* launches) {
+    if (total_ms == nullptr || launches == nullptr)
+        return fail(TG_ERR_INVALID_ARGUMENT, "total_ms or launches is NULL");
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
+    {
+        std::lock_guard<std::mutex> lk(g_timing_mu);
+        evs.swap(g_timing_events);
+    }
+    double sum = 0.0;
+    int rc = TG_OK;
+    for (auto& e : evs) {
+        float ms = 0.0f;
+        hipError_t err = hipEventSynchronize(e.second);
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, e.first, e.second);
+        if (err != hipSuccess && rc == TG_OK) rc = hip_fail(err, "hipEventElapsedTime");
+        sum += ms;
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+    }
+    *total_ms = sum;
+    *launches = int64_t(evs.size());
+    return rc;
 }
 
 int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout, const void* A,
