@@ -375,3 +375,37 @@ def test_full_tile_strided_batched():
         bt = b[t * sb: t * sb + k * n].reshape(k, n)
         assert_exact(c_np[t * sc: t * sc + m * n].reshape(m, n),
                      am_np[t * sc: t * sc + m * n].reshape(m, n), *oracle.gemm("maxplus", at, bt))
+
+
+# Argmax problems with at least 1536 tiles of 64 x 128 take the wide-tile
+# kernel; small K keeps the oracle cheap.
+WIDE_SHAPES = [(3072, 32, 4096), (1536, 96, 8192)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_wide_tile_argmax(sr, dt):
+    rng = np.random.default_rng(400 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in WIDE_SHAPES:
+        print(f"[case] wide-tile {sr} {dt} m={m} k={k} n={n}", flush=True)
+        if dt == "i32":
+            a = rng.integers(-5, 6, size=(m, k)).astype(dtype)  # many ties
+            b = rng.integers(-5, 6, size=(k, n)).astype(dtype)
+        else:
+            a = tc.rng_matrix(rng, dtype, (m, k))
+            b = tc.rng_matrix(rng, dtype, (k, n))
+        c, am = gpu_gemm(sr, a, b, True)
+        assert_exact(c, am, *oracle.gemm(sr, a, b))
+
+
+def test_wide_tile_argmax_batched():
+    from tropical_gemm import ops
+
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((12, 512, 64)).astype(np.float32)
+    b = rng.standard_normal((12, 64, 2048)).astype(np.float32)
+    c, am = ops.gemm_batched("minplus", _dev(a), _dev(b), True)
+    c, am = c.cpu().numpy(), am.cpu().numpy()
+    for t in range(12):
+        assert_exact(c[t], am[t], *oracle.gemm("minplus", a[t], b[t]))

@@ -22,12 +22,60 @@
 
 namespace tg {
 
+// Tile configurations: 16 x 16 threads, 4 x TN outputs per thread.
+//   TN = 8: 64 x 128 tiles; argmax held to 3 waves/SIMD (<= 168 VGPRs),
+//           value-only at 2 (its schedule wants ~200 VGPRs).
+//   TN = 4: 64 x 64 tiles, 4 waves/SIMD (<= 128 VGPRs): twice the tiles, so
+//           4096^2 outputs make exactly 4 rounds of 1024 resident workgroups.
+template <int TN_>
 struct DlCfg {
-    static constexpr int BM = 64, BN = 128, BK = TG_CHUNK, TM = 4, TN = 8;
+    static constexpr int BM = 64, BN = 16 * TN_, BK = TG_CHUNK, TM = 4, TN = TN_;
+    static constexpr int WAVES_ARGMAX = TN_ == 8 ? 3 : 4;
+    static constexpr int WAVES_VALUE = TN_ == 8 ? 2 : 4;
+    static constexpr int NBI = BK * BN / 1024;      // 1 KB B-tile loads per wave
+    static constexpr int RPI = 256 / BN;            // B k-rows per 1 KB load
+    static constexpr int LPR = BN / 4;              // lanes per B k-row
     static constexpr int A_BYTES = BM * BK * 4;   // one A buffer
     static constexpr int B_BYTES = BK * BN * 4;   // one B buffer
-    static constexpr int LDS_BYTES = 2 * (A_BYTES + B_BYTES);
+    static constexpr int TILE_BYTES = 2 * (A_BYTES + B_BYTES);
+    // Argmax epilogue, reusing the tile buffers: bucket counts, per-output
+    // chunk (u16), chunk-sorted output list (u16), per-output result (u8),
+    // then a few words of scan scratch past the tile buffers.
+    static constexpr int OUTS = BM * BN;            // outputs per tile
+    static constexpr int NB_MAX = 2048;             // chunk buckets
+    static constexpr int HIST_OFF = 0;
+    static constexpr int CHS_OFF = HIST_OFF + NB_MAX * 4;
+    static constexpr int LIST_OFF = CHS_OFF + OUTS * 2;
+    static constexpr int RES_OFF = LIST_OFF + OUTS * 2;
+    static constexpr int MISC_OFF = RES_OFF + OUTS;
+    static constexpr int LDS_BYTES = (MISC_OFF + 64 > TILE_BYTES) ? MISC_OFF + 64 : TILE_BYTES;
+    static_assert(MISC_OFF <= TILE_BYTES, "epilogue arrays must fit in the tile buffers");
 };
+
+// Exclusive prefix sum over the 256 threads of a workgroup; returns the
+// exclusive prefix of x and sets total.  scratch: 5 ints of LDS.
+__device__ __forceinline__ int block_exclusive_scan(int x, int* scratch, int& total) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int inc = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+    }
+    if (lane == 63) scratch[wave] = inc;
+    __syncthreads();
+    int before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int t = scratch[w];
+        if (w < wave) before += t;
+        total += t;
+    }
+    __syncthreads();
+    return before + inc - x;
+}
 
 // One 16-byte direct load per lane: global src -> LDS at dst + lane * 16
 // (dst must be the same for the whole wave).  A non-template wrapper: the
@@ -37,24 +85,34 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// True when tg_gemm_dl can run the problem.
-inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, const void* A,
-                    const void* B) {
-    return M > 0 && N > 0 && K > 0 && M % DlCfg::BM == 0 && N % DlCfg::BN == 0 &&
-           K % DlCfg::BK == 0 && sA % 4 == 0 && sB % 4 == 0 &&
-           (reinterpret_cast<uintptr_t>(A) & 15u) == 0 && (reinterpret_cast<uintptr_t>(B) & 15u) == 0;
+// True when tg_gemm_dl<.., TN> can run the problem: full tiles, 16-byte
+// aligned operands, outputs and batch strides (tiles load and store 16 bytes
+// per lane), and chunk indices that fit the epilogue's 16-bit slots.
+template <int TN>
+inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC,
+                    const void* A, const void* B, const void* C, const void* IDX) {
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    using Cfg = DlCfg<TN>;
+    return M > 0 && N > 0 && K > 0 && M % Cfg::BM == 0 && N % Cfg::BN == 0 &&
+           K % Cfg::BK == 0 && K / Cfg::BK < 0xFFFF && sA % 4 == 0 && sB % 4 == 0 &&
+           sC % 4 == 0 && a16(A) && a16(B) && a16(C) && (IDX == nullptr || a16(IDX));
 }
 
-template <int SR, typename T, bool ARGMAX>
-__global__ __launch_bounds__(TG_THREADS) void tg_gemm_dl(
+// Waves per SIMD come from the tile configuration (DlCfg): other resident
+// waves hide the LDS latency of the main loop.
+template <int SR, typename T, bool ARGMAX, int TN_>
+__global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
+    ARGMAX ? DlCfg<TN_>::WAVES_ARGMAX : DlCfg<TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
     int64_t sB, int64_t sC, int tiles_m, int tiles_n) {
     static_assert(sizeof(T) == 4, "direct-to-LDS kernel is for 32-bit types");
-    constexpr int BM = DlCfg::BM, BN = DlCfg::BN, BK = DlCfg::BK, TM = DlCfg::TM, TN = DlCfg::TN;
+    using Cfg = DlCfg<TN_>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, TM = Cfg::TM, TN = Cfg::TN;
+    constexpr int NBI = Cfg::NBI;
     extern __shared__ __align__(16) unsigned char dl_lds[];
     T* const As0 = reinterpret_cast<T*>(dl_lds);
-    T* const Bs0 = reinterpret_cast<T*>(dl_lds + 2 * DlCfg::A_BYTES);
+    T* const Bs0 = reinterpret_cast<T*>(dl_lds + 2 * Cfg::A_BYTES);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -75,8 +133,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_dl(
     }
 
     // Per-lane global sources of this wave's direct loads (chunk 0).  A: 8
-    // rows per 1 KB instruction, wave w issues instructions 2w, 2w+1.  B: 2
-    // k-rows per instruction, wave w issues 4w .. 4w+3.
+    // rows per 1 KB instruction, wave w issues instructions 2w, 2w+1.  B:
+    // RPI k-rows per instruction, wave w issues NBI*w .. NBI*w + NBI-1.
     const T* srcA[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -85,11 +143,11 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_dl(
         const int qsrc = qpos ^ ((r >> 2) & 7);
         srcA[q] = A + (row0 + r) * K + qsrc * 4;
     }
-    const T* srcB[4];
+    const T* srcB[NBI];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int kr = (wave * 4 + q) * 2 + (lane >> 5);
-        srcB[q] = B + int64_t(kr) * N + col0 + (lane & 31) * 4;
+    for (int q = 0; q < NBI; ++q) {
+        const int kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
+        srcB[q] = B + int64_t(kr) * N + col0 + (lane % Cfg::LPR) * 4;
     }
     auto issue_loads = [&](int64_t t, int buf) {
         T* adst = As0 + buf * (BM * BK);
@@ -98,8 +156,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_dl(
         for (int q = 0; q < 2; ++q)
             lds_load16(srcA[q] + t * BK, adst + (wave * 2 + q) * 256);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            lds_load16(srcB[q] + t * BK * N, bdst + (wave * 4 + q) * 256);
+        for (int q = 0; q < NBI; ++q)
+            lds_load16(srcB[q] + t * BK * N, bdst + (wave * NBI + q) * 256);
     };
 
     T acc[TM][TN];
@@ -175,47 +233,173 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_dl(
     }
 
     // ---- epilogue ------------------------------------------------------------
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    // Output (i, j) of this thread: tile row ty*4+i, tile column (j>>2)*64 +
+    // tx*4 + (j&3); its local id is row*BN + column.
+    auto store_row = [&](int i, const T (&v)[TN], const int32_t (&ix)[TN]) {
         const int64_t gr = row0 + ty * 4 + i;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int64_t gc = col0 + (j >> 2) * 64 + tx * 4 + (j & 3);
-            T val = acc[i][j];
-            int32_t idx = 0;
+        for (int g = 0; g < TN / 4; ++g) {
+            const int64_t gc = col0 + g * 64 + tx * 4;
+            Vec16<T> cv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cv.v[e] = v[g * 4 + e];
+            *reinterpret_cast<Vec16<T>*>(C + gr * N + gc) = cv;
             if constexpr (ARGMAX) {
-                // Exact first k inside the recorded chunk (see tg_gemm_tiles).
-                constexpr int NW = BK / 4;
-                const int64_t c = ch[i][j] < 0 ? 0 : ch[i][j];
-                const T* ap = A + gr * K + c * BK;
-                const T* bp = BT + gc * K + c * BK;
-                Vec16<T> av[NW], bv[NW];
+                Vec16<int32_t> iv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) iv.v[e] = ix[g * 4 + e];
+                *reinterpret_cast<Vec16<int32_t>*>(IDX + gr * N + gc) = iv;
+            }
+        }
+    };
+    if constexpr (!ARGMAX) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            int32_t none[TN] = {};
+            store_row(i, acc[i], none);
+        }
+    } else {
+        // Exact first k inside each output's recorded chunk c.  The window of
+        // chunk c holds the final value as its own maximum (no product of an
+        // earlier chunk reaches it), so the window alone gives the target and
+        // the first k attaining it.  Outputs are resolved in chunk order
+        // (LDS counting sort), so workgroups running side by side read the
+        // same A-row / B^T-row segments at about the same time and mostly hit
+        // in cache.  The resolve returns the offset inside the chunk and, for
+        // a zero maximum, the sign of the first zero product (the CPU keeps
+        // the first occurrence's bits).
+        constexpr uint16_t NONE = 0xFFFF;
+        uint32_t* hist = reinterpret_cast<uint32_t*>(dl_lds + Cfg::HIST_OFF);
+        uint16_t* chs = reinterpret_cast<uint16_t*>(dl_lds + Cfg::CHS_OFF);
+        uint16_t* list = reinterpret_cast<uint16_t*>(dl_lds + Cfg::LIST_OFF);
+        uint8_t* res = dl_lds + Cfg::RES_OFF;
+        int* misc = reinterpret_cast<int*>(dl_lds + Cfg::MISC_OFF);
+        // Buckets: chunk >> shift, at most NB_MAX of them.
+        int shift = 0;
+        while (((ntiles - 1) >> shift) >= Cfg::NB_MAX) ++shift;
+        const int nb = int(((ntiles - 1) >> shift) + 1);
+
+        __syncthreads();  // every wave is done with the tile buffers
+        for (int b = tid; b < nb; b += TG_THREADS) hist[b] = 0;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
+                chs[lid] = ch[i][j] < 0 ? NONE : uint16_t(ch[i][j]);
+            }
+        __syncthreads();
+        uint16_t rank[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                rank[i][j] = ch[i][j] < 0 ? 0 : uint16_t(atomicAdd(&hist[ch[i][j] >> shift], 1u));
+        __syncthreads();
+        // Exclusive scan of the bucket counts, 8 buckets per thread.
+        constexpr int PER = Cfg::NB_MAX / TG_THREADS;
+        int cnt[PER];
+        int mine = 0;
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int b = tid * PER + q;
+            cnt[q] = b < nb ? int(hist[b]) : 0;
+            mine += cnt[q];
+        }
+        int total = 0;
+        int run = block_exclusive_scan(mine, misc, total);
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+            const int b = tid * PER + q;
+            if (b < nb) hist[b] = uint32_t(run);
+            run += cnt[q];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                if (ch[i][j] >= 0) {
+                    const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
+                    list[hist[ch[i][j] >> shift] + rank[i][j]] = uint16_t(lid);
+                }
+            }
+        __syncthreads();
+
+        // Resolve, chunk-sorted, one output per thread at a time (two in
+        // flight would push the kernel past the 3-waves-per-SIMD register
+        // budget of the main loop).
+        constexpr int NW = BK / 4;
+        constexpr int G = 1;
+        for (int e0 = 0; e0 < total; e0 += TG_THREADS * G) {
+            int lid[G];
+            int64_t c[G];
+            bool valid[G];
+            Vec16<T> av[G][NW], bv[G][NW];
+            const T* ap[G];
+            const T* bp[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int e = e0 + g * TG_THREADS + tid;
+                valid[g] = e < total;
+                lid[g] = valid[g] ? int(list[e]) : 0;
+                c[g] = valid[g] ? int64_t(chs[lid[g]]) : 0;
+                ap[g] = A + (row0 + lid[g] / BN) * K + c[g] * BK;
+                bp[g] = BT + (col0 + (lid[g] & (BN - 1))) * K + c[g] * BK;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
-                    av[w] = reinterpret_cast<const Vec16<T>*>(ap)[w];
-                    bv[w] = reinterpret_cast<const Vec16<T>*>(bp)[w];
+                    av[g][w] = reinterpret_cast<const Vec16<T>*>(ap[g])[w];
+                    bv[g][w] = reinterpret_cast<const Vec16<T>*>(bp[g])[w];
                 }
-                int32_t f = 0;
+            }
 #pragma unroll
-                for (int qd = BK / 8 - 1; qd >= 0; --qd) {
+            for (int g = 0; g < G; ++g) {
+                T p[BK];
 #pragma unroll
-                    for (int kk = qd * 8 + 7; kk >= qd * 8; --kk) {
-                        const T p = tmul<SR, T>(av[kk >> 2].v[kk & 3], bv[kk >> 2].v[kk & 3]);
-                        f = (p == val) ? kk : f;
-                    }
+                for (int kk = 0; kk < BK; ++kk)
+                    p[kk] = tmul<SR, T>(av[g][kk >> 2].v[kk & 3], bv[g][kk >> 2].v[kk & 3]);
+                T mx = tjoin<SR, T>(p[0], p[1]);
+#pragma unroll
+                for (int kk = 2; kk < BK; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
+                // Last match scanning downwards == first match; groups of 8
+                // compares keep few lane masks live at once.
+                int f = 0;
+#pragma unroll
+                for (int q = BK / 8 - 1; q >= 0; --q) {
+#pragma unroll
+                    for (int kk = q * 8 + 7; kk >= q * 8; --kk) f = (p[kk] == mx) ? kk : f;
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                idx = int32_t(c * BK + f);
+                int r = f;
                 if constexpr (std::is_floating_point<T>::value) {
-                    if (val == T(0)) val = tmul<SR, T>(ap[f], bp[f]);
+                    if (mx == T(0) && __builtin_signbit(tmul<SR, T>(ap[g][f], bp[g][f]))) r |= 32;
                 }
-                if (ch[i][j] < 0) {
-                    val = tzero<SR, T>();
-                    idx = 0;
-                }
-                IDX[gr * N + gc] = idx;
+                if (valid[g]) res[lid[g]] = uint8_t(r);
             }
-            C[gr * N + gc] = val;
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            T v[TN];
+            int32_t ix[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
+                const uint16_t cc = chs[lid];
+                if (cc == NONE) {  // the tropical zero was never beaten
+                    v[j] = tzero<SR, T>();
+                    ix[j] = 0;
+                } else {
+                    const int r = res[lid];
+                    ix[j] = int32_t(cc) * BK + (r & 31);
+                    v[j] = acc[i][j];
+                    if constexpr (std::is_floating_point<T>::value) {
+                        if (v[j] == T(0)) v[j] = (r & 32) ? -T(0) : T(0);
+                    }
+                }
+            }
+            store_row(i, v, ix);
         }
     }
 }
