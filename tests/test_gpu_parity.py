@@ -297,7 +297,9 @@ def test_context_and_memory_entry_points():
 # K % 32 == 0 take the direct-to-LDS kernel; these pin it to the oracle.
 # ---------------------------------------------------------------------------
 
-ALIGNED_SHAPES = [(64, 32, 128), (128, 160, 256), (320, 1024, 384), (64, 4096, 128)]
+# K <= 192 resolves argmax in chunks of 8, K <= 768 in chunks of 16, else 32.
+ALIGNED_SHAPES = [(64, 32, 128), (128, 160, 256), (192, 512, 256), (64, 768, 128),
+                  (320, 1024, 384), (64, 4096, 128)]
 
 
 @pytest.mark.parametrize("dt", ["f32", "i32"])
@@ -318,11 +320,12 @@ def test_full_tile_shapes(sr, dt):
 
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
 @pytest.mark.parametrize("dt", ["f32", "i32"])
-def test_full_tile_heavy_ties(sr, dt):
+@pytest.mark.parametrize("k", [96, 320, 1056])
+def test_full_tile_heavy_ties(sr, dt, k):
     rng = np.random.default_rng(78)
     dtype = tc.NP_DTYPES[dt]
-    a = rng.integers(0, 3, size=(128, 320)).astype(dtype)
-    b = rng.integers(0, 3, size=(320, 256)).astype(dtype)
+    a = rng.integers(0, 3, size=(128, k)).astype(dtype)
+    b = rng.integers(0, 3, size=(k, 256)).astype(dtype)
     c, am = gpu_gemm(sr, a, b)
     assert_exact(c, am, *oracle.gemm(sr, a, b))
 
@@ -377,9 +380,9 @@ def test_full_tile_strided_batched():
                      am_np[t * sc: t * sc + m * n].reshape(m, n), *oracle.gemm("maxplus", at, bt))
 
 
-# Argmax problems with at least 1536 tiles of 64 x 128 take the wide-tile
-# kernel; small K keeps the oracle cheap.
-WIDE_SHAPES = [(3072, 32, 4096), (1536, 96, 8192)]
+# Argmax problems with K > 768 and at least 1536 tiles of 64 x 128 take the
+# wide-tile kernel.
+WIDE_SHAPES = [(3072, 800, 4096), (1536, 1024, 8192)]
 
 
 @pytest.mark.parametrize("dt", ["f32", "i32"])
@@ -403,8 +406,8 @@ def test_wide_tile_argmax_batched():
     from tropical_gemm import ops
 
     rng = np.random.default_rng(41)
-    a = rng.standard_normal((12, 512, 64)).astype(np.float32)
-    b = rng.standard_normal((12, 64, 2048)).astype(np.float32)
+    a = rng.standard_normal((12, 512, 800)).astype(np.float32)
+    b = rng.standard_normal((12, 800, 2048)).astype(np.float32)
     c, am = ops.gemm_batched("minplus", _dev(a), _dev(b), True)
     c, am = c.cpu().numpy(), am.cpu().numpy()
     for t in range(12):

@@ -174,7 +174,7 @@ struct Problem {
 };
 
 // Direct-to-LDS kernel for 32-bit types when every tile is full.
-template <int SR, typename T, int TN>
+template <int SR, typename T, int TN, int CL>
 int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
     using Cfg = tg::DlCfg<TN>;
     const int64_t tiles_m = p.M / Cfg::BM;
@@ -200,12 +200,12 @@ int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
                                p.sB, p.K * p.N);
             TG_HIP(hipGetLastError());
             KernelTimer timer(st);
-            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN>), grid, dim3(256), Cfg::LDS_BYTES, st,
+            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
                                Az, Bz, BT, Cz, p.IDX + z0 * p.sC, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                int(tiles_m), int(tiles_n));
         } else {
             KernelTimer timer(st);
-            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN>), grid, dim3(256), Cfg::LDS_BYTES, st,
+            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
                                Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                int(tiles_m), int(tiles_n));
         }
@@ -217,16 +217,25 @@ int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
     if constexpr (sizeof(T) == 4) {
+        // Argmax chunk length: bookkeeping costs ~3 ops per output per chunk
+        // (3K/CL) and the exact resolve ~4 ops per product of one chunk
+        // (4*CL); the sum is smallest near CL = sqrt(3K/4).
+        const bool argmax = p.IDX != nullptr;
+        const int cl = !argmax ? 32 : p.K <= 192 ? 8 : p.K <= 768 ? 16 : 32;
         // 64 x 128 tiles for argmax problems big enough that the last round
         // of 768 resident workgroups is a small share of the work (their
         // main loop is the faster one); 64 x 64 tiles otherwise (value-only
         // runs four workgroups per CU, small problems get twice the tiles).
-        const bool wide = p.IDX != nullptr && p.N % tg::DlCfg<8>::BN == 0 &&
+        const bool wide = argmax && cl == 32 && p.N % tg::DlCfg<8>::BN == 0 &&
                           (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
-        if (wide && tg::dl_fits<8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 8>(p, ws, st);
-        if (tg::dl_fits<4>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4>(p, ws, st);
+        if (wide && tg::dl_fits<8, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_dl<SR, T, 8, 32>(p, ws, st);
+        if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_dl<SR, T, 4, 8>(p, ws, st);
+        if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_dl<SR, T, 4, 16>(p, ws, st);
+        if (cl == 32 && tg::dl_fits<4, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_dl<SR, T, 4, 32>(p, ws, st);
     }
     using Cfg = tg::TileCfg<T>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;

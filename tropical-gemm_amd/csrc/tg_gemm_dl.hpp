@@ -85,22 +85,22 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// True when tg_gemm_dl<.., TN> can run the problem: full tiles, 16-byte
+// True when tg_gemm_dl<.., TN, CL> can run the problem: full tiles, 16-byte
 // aligned operands, outputs and batch strides (tiles load and store 16 bytes
 // per lane), and chunk indices that fit the epilogue's 16-bit slots.
-template <int TN>
+template <int TN, int CL>
 inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC,
                     const void* A, const void* B, const void* C, const void* IDX) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     using Cfg = DlCfg<TN>;
     return M > 0 && N > 0 && K > 0 && M % Cfg::BM == 0 && N % Cfg::BN == 0 &&
-           K % Cfg::BK == 0 && K / Cfg::BK < 0xFFFF && sA % 4 == 0 && sB % 4 == 0 &&
+           K % Cfg::BK == 0 && K / CL < 0xFFFF && sA % 4 == 0 && sB % 4 == 0 &&
            sC % 4 == 0 && a16(A) && a16(B) && a16(C) && (IDX == nullptr || a16(IDX));
 }
 
 // Waves per SIMD come from the tile configuration (DlCfg): other resident
 // waves hide the LDS latency of the main loop.
-template <int SR, typename T, bool ARGMAX, int TN_>
+template <int SR, typename T, bool ARGMAX, int TN_, int CL>
 __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     ARGMAX ? DlCfg<TN_>::WAVES_ARGMAX : DlCfg<TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
@@ -110,6 +110,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     using Cfg = DlCfg<TN_>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, TM = Cfg::TM, TN = Cfg::TN;
     constexpr int NBI = Cfg::NBI;
+    static_assert(CL == 8 || CL == 16 || CL == 32, "argmax chunk of 8, 16 or 32 k");
     extern __shared__ __align__(16) unsigned char dl_lds[];
     T* const As0 = reinterpret_cast<T*>(dl_lds);
     T* const Bs0 = reinterpret_cast<T*>(dl_lds + 2 * Cfg::A_BYTES);
@@ -197,39 +198,45 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         __syncthreads();
         if (t + 1 < ntiles) issue_loads(t + 1, buf ^ 1);
 
-        T cm[TM][TN];
-        {
-            T a[TM][2], b[2][TN];
-            load_frag(buf, 0, a, b);
+        // The LDS tile holds BK / CL argmax chunks of CL consecutive k.
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+        for (int s = 0; s < BK / CL; ++s) {
+            T cm[TM][TN];
+            {
+                T a[TM][2], b[2][TN];
+                load_frag(buf, s * CL, a, b);
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a[i][0], b[0][j]), tmul<SR, T>(a[i][1], b[1][j]));
-        }
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int kk = 2; kk < BK; kk += 2) {
-            T a[TM][2], b[2][TN];
-            load_frag(buf, kk, a, b);
+                    for (int j = 0; j < TN; ++j)
+                        cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a[i][0], b[0][j]),
+                                                tmul<SR, T>(a[i][1], b[1][j]));
+            }
+#pragma unroll
+            for (int kk = s * CL + 2; kk < (s + 1) * CL; kk += 2) {
+                T a[TM][2], b[2][TN];
+                load_frag(buf, kk, a, b);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
+                        const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
+                        cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
+                    }
+            }
+            // Strict improvement only (the reference's "keep acc iff acc >= p").
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
-                    const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
-                    cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
+                    if constexpr (ARGMAX) {
+                        if (tbetter<SR, T>(cm[i][j], acc[i][j]))
+                            ch[i][j] = int32_t(t * (BK / CL) + s);
+                    }
+                    acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
                 }
         }
-        // Strict improvement only (the reference's "keep acc iff acc >= p").
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                if constexpr (ARGMAX) {
-                    if (tbetter<SR, T>(cm[i][j], acc[i][j])) ch[i][j] = int32_t(t);
-                }
-                acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
-            }
     }
 
     // ---- epilogue ------------------------------------------------------------
@@ -275,9 +282,10 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         uint8_t* res = dl_lds + Cfg::RES_OFF;
         int* misc = reinterpret_cast<int*>(dl_lds + Cfg::MISC_OFF);
         // Buckets: chunk >> shift, at most NB_MAX of them.
+        const int64_t nchunks = K / CL;
         int shift = 0;
-        while (((ntiles - 1) >> shift) >= Cfg::NB_MAX) ++shift;
-        const int nb = int(((ntiles - 1) >> shift) + 1);
+        while (((nchunks - 1) >> shift) >= Cfg::NB_MAX) ++shift;
+        const int nb = int(((nchunks - 1) >> shift) + 1);
 
         __syncthreads();  // every wave is done with the tile buffers
         for (int b = tid; b < nb; b += TG_THREADS) hist[b] = 0;
@@ -329,7 +337,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         // Resolve, chunk-sorted, one output per thread at a time (two in
         // flight would push the kernel past the 3-waves-per-SIMD register
         // budget of the main loop).
-        constexpr int NW = BK / 4;
+        constexpr int NW = CL / 4;
         constexpr int G = 1;
         for (int e0 = 0; e0 < total; e0 += TG_THREADS * G) {
             int lid[G];
@@ -344,8 +352,8 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 valid[g] = e < total;
                 lid[g] = valid[g] ? int(list[e]) : 0;
                 c[g] = valid[g] ? int64_t(chs[lid[g]]) : 0;
-                ap[g] = A + (row0 + lid[g] / BN) * K + c[g] * BK;
-                bp[g] = BT + (col0 + (lid[g] & (BN - 1))) * K + c[g] * BK;
+                ap[g] = A + (row0 + lid[g] / BN) * K + c[g] * CL;
+                bp[g] = BT + (col0 + (lid[g] & (BN - 1))) * K + c[g] * CL;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
                     av[g][w] = reinterpret_cast<const Vec16<T>*>(ap[g])[w];
@@ -354,18 +362,18 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                T p[BK];
+                T p[CL];
 #pragma unroll
-                for (int kk = 0; kk < BK; ++kk)
+                for (int kk = 0; kk < CL; ++kk)
                     p[kk] = tmul<SR, T>(av[g][kk >> 2].v[kk & 3], bv[g][kk >> 2].v[kk & 3]);
                 T mx = tjoin<SR, T>(p[0], p[1]);
 #pragma unroll
-                for (int kk = 2; kk < BK; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
+                for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
                 // Last match scanning downwards == first match; groups of 8
                 // compares keep few lane masks live at once.
                 int f = 0;
 #pragma unroll
-                for (int q = BK / 8 - 1; q >= 0; --q) {
+                for (int q = CL / 8 - 1; q >= 0; --q) {
 #pragma unroll
                     for (int kk = q * 8 + 7; kk >= q * 8; --kk) f = (p[kk] == mx) ? kk : f;
                     __builtin_amdgcn_sched_barrier(0);
@@ -392,7 +400,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                     ix[j] = 0;
                 } else {
                     const int r = res[lid];
-                    ix[j] = int32_t(cc) * BK + (r & 31);
+                    ix[j] = int32_t(cc) * CL + (r & 31);
                     v[j] = acc[i][j];
                     if constexpr (std::is_floating_point<T>::value) {
                         if (v[j] == T(0)) v[j] = (r & 32) ? -T(0) : T(0);
