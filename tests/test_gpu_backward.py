@@ -47,7 +47,8 @@ def _contrib(argmax, g, k, which, other=None):
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
-@pytest.mark.parametrize("shape", [(37, 23, 29), (130, 300, 70), (5, 1, 9), (64, 9000, 3)])
+@pytest.mark.parametrize("shape", [(37, 23, 29), (130, 300, 70), (5, 1, 9), (64, 9000, 3),
+                                   (3, 40000, 5), (200, 128, 700)])
 def test_backward_matches_oracle(dtype, sr, shape):
     from tropical_gemm import ops
 

@@ -436,20 +436,55 @@ int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t b
     return TG_OK;
 }
 
+// LDS capacities (elements) of the two column-block kernel variants.
+template <typename T>
+struct ColsLds {
+    static constexpr int SMALL = 32768 / int(sizeof(T));   // 32 KB: several workgroups per CU
+    static constexpr int LARGE = 131072 / int(sizeof(T));  // 128 KB: one workgroup per CU
+};
+
 template <typename T, bool MULT>
 int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sB, hipStream_t st) {
-    for (int64_t z = 0; z < batch; ++z) {
-        int rc = launch_fill_zero(GB + z * sB, size_t(K * N) * sizeof(T), st);
-        if (rc != TG_OK) return rc;
+    // Column block: the widest power of two <= 64 whose K x BJ block fits.
+    auto block_log2 = [&](int64_t cap) {
+        int l = 0;
+        while (l < 6 && K * (int64_t(2) << l) <= cap) ++l;
+        return K <= cap ? l : -1;
+    };
+    int lsmall = block_log2(ColsLds<T>::SMALL);
+    int llarge = block_log2(ColsLds<T>::LARGE);
+    const bool use_small = lsmall >= 3;  // at least 8 columns per block
+    const int l = use_small ? lsmall : llarge;
+    if (l < 0) {
+        // K too large for LDS blocks: global atomics into a zeroed grad_B.
+        for (int64_t z = 0; z < batch; ++z) {
+            int rc = launch_fill_zero(GB + z * sB, size_t(K * N) * sizeof(T), st);
+            if (rc != TG_OK) return rc;
+        }
+        if (M * N == 0) return TG_OK;
+        for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
+            const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
+            const int64_t blocks = (M * N + 255) / 256;
+            hipLaunchKernelGGL((tg::tg_backward_cols<T, MULT>), dim3(unsigned(blocks), 1, unsigned(nb)),
+                               dim3(256), 0, st, G + z0 * sC, I + z0 * sC,
+                               MULT ? O + z0 * sO : nullptr, GB + z0 * sB, M, N, K, sC, sO, sB);
+            TG_HIP(hipGetLastError());
+        }
+        return TG_OK;
     }
-    if (M * N == 0) return TG_OK;
+    const int64_t nblocks = (N + (int64_t(1) << l) - 1) >> l;
     for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
         const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
-        const int64_t blocks = (M * N + 255) / 256;
-        hipLaunchKernelGGL((tg::tg_backward_cols<T, MULT>), dim3(unsigned(blocks), 1, unsigned(nb)),
-                           dim3(256), 0, st, G + z0 * sC, I + z0 * sC,
-                           MULT ? O + z0 * sO : nullptr, GB + z0 * sB, M, N, K, sC, sO, sB);
+        const T* Oz = MULT ? O + z0 * sO : nullptr;
+        if (use_small)
+            hipLaunchKernelGGL((tg::tg_backward_cols_lds<T, MULT, ColsLds<T>::SMALL>),
+                               dim3(unsigned(nblocks), 1, unsigned(nb)), dim3(512), 0, st, G + z0 * sC,
+                               I + z0 * sC, Oz, GB + z0 * sB, M, N, K, sC, sO, sB, l);
+        else
+            hipLaunchKernelGGL((tg::tg_backward_cols_lds<T, MULT, ColsLds<T>::LARGE>),
+                               dim3(unsigned(nblocks), 1, unsigned(nb)), dim3(512), 0, st, G + z0 * sC,
+                               I + z0 * sC, Oz, GB + z0 * sB, M, N, K, sC, sO, sB, l);
         TG_HIP(hipGetLastError());
     }
     return TG_OK;

@@ -6,7 +6,9 @@
 //                       TROPICAL_GEMM_ARGMAX_* 526-996, batched 1094-1219)
 //   tg_transpose       B -> B^T staging for the argmax epilogue (new)
 //   tg_backward_rows   grad_A scatter (TROPICAL_BACKWARD_A 1002-1018)
-//   tg_backward_cols   grad_B scatter (TROPICAL_BACKWARD_B 1020-1036)
+//   tg_backward_cols_lds  grad_B scatter into LDS column blocks
+//                      (TROPICAL_BACKWARD_B 1020-1036)
+//   tg_backward_cols   grad_B fallback with global atomics (huge K)
 //   tg_fill_zero       zero fill used instead of hipMemsetAsync
 //
 // All matrices are row-major here; the host layer maps column-major calls
@@ -467,12 +469,24 @@ __global__ __launch_bounds__(256) void tg_backward_rows(const T* __restrict__ G,
     if (MULT) OTHER += z * sO;
     for (int64_t k = threadIdx.x; k < K; k += 256) row[k] = T(0);
     __syncthreads();
-    for (int64_t j = threadIdx.x; j < N; j += 256) {
-        const int32_t kk = IDX[i * N + j];
-        if (kk >= 0 && int64_t(kk) < K) {
-            T g = G[i * N + j];
-            if (MULT) g = g * OTHER[int64_t(kk) * N + j];
-            atomicAdd(&row[kk], g);
+    // U entries per thread per pass, all loads issued before the LDS adds.
+    constexpr int U = 8;
+    for (int64_t j0 = 0; j0 < N; j0 += 256 * U) {
+        int32_t kk[U];
+        T g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t j = j0 + u * 256 + threadIdx.x;
+            kk[u] = j < N ? IDX[i * N + j] : -1;
+            g[u] = j < N ? G[i * N + j] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (kk[u] >= 0 && int64_t(kk[u]) < K) {
+                T v = g[u];
+                if (MULT) v = v * OTHER[int64_t(kk[u]) * N + j0 + u * 256 + threadIdx.x];
+                atomicAdd(&row[kk[u]], v);
+            }
         }
     }
     __syncthreads();
@@ -529,6 +543,67 @@ __global__ __launch_bounds__(256) void tg_backward_cols(const T* __restrict__ G,
         T g = G[o];
         if (MULT) g = g * OTHER[i * K + kk];
         unsafeAtomicAdd(&GB[int64_t(kk) * N + j], g);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// grad_B for a block of BJ = 2^bj_log2 consecutive columns, accumulated in
+// LDS (K x BJ values, at most LDS_ELEMS) and written out whole: no global
+// atomics and no separate zero fill.  Consecutive column blocks share cache
+// lines, so the block order is remapped to keep neighbours on one XCD.
+//   MULT=true: MaxMul rule, g *= A[i, kk]  (OTHER = A, row-major M x K).
+// grid = (ceil(N / BJ), 1, batch), block = 512.
+// ---------------------------------------------------------------------------
+template <typename T, bool MULT, int LDS_ELEMS>
+__global__ __launch_bounds__(512) void tg_backward_cols_lds(const T* __restrict__ G,
+                                                            const int32_t* __restrict__ IDX,
+                                                            const T* __restrict__ OTHER,
+                                                            T* __restrict__ GB, int64_t M, int64_t N,
+                                                            int64_t K, int64_t sC, int64_t sO,
+                                                            int64_t sB, int bj_log2) {
+    __shared__ T acc[LDS_ELEMS];
+    const int BJ = 1 << bj_log2;
+    const int nblocks = int(gridDim.x);
+    int bid = int(blockIdx.x);
+    if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
+    const int64_t j0 = int64_t(bid) * BJ;
+    const int64_t z = blockIdx.z;
+    G += z * sC;
+    IDX += z * sC;
+    GB += z * sB;
+    if (MULT) OTHER += z * sO;
+    const int64_t total = K * BJ;
+    for (int64_t e = threadIdx.x; e < total; e += 512) acc[e] = T(0);
+    __syncthreads();
+    // Entries (i, c), c fastest: consecutive lanes read consecutive columns.
+    constexpr int U = 8;
+    const int64_t ne = M * BJ;
+    for (int64_t e0 = 0; e0 < ne; e0 += 512 * U) {
+        int32_t kk[U];
+        T g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t e = e0 + u * 512 + threadIdx.x;
+            const int64_t i = e >> bj_log2;
+            const int64_t j = j0 + (e & (BJ - 1));
+            const bool ok = e < ne && j < N;
+            kk[u] = ok ? IDX[i * N + j] : -1;
+            g[u] = ok ? G[i * N + j] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (kk[u] >= 0 && int64_t(kk[u]) < K) {
+                const int64_t e = e0 + u * 512 + threadIdx.x;
+                T v = g[u];
+                if (MULT) v = v * OTHER[(e >> bj_log2) * K + kk[u]];
+                atomicAdd(&acc[int64_t(kk[u]) * BJ + (e & (BJ - 1))], v);
+            }
+        }
+    }
+    __syncthreads();
+    for (int64_t e = threadIdx.x; e < total; e += 512) {
+        const int64_t j = j0 + (e & (BJ - 1));
+        if (j < N) GB[(e >> bj_log2) * N + j] = acc[e];
     }
 }
 
