@@ -46,6 +46,7 @@ WORKLOAD_NAMES = {
     "C2": "C2: MinPlus f32 4096^3 +argmax, 10% +inf, zero diagonal",
     "C3": "C3: MaxMul f32 8192x2048x4096 value-only",
     "C4": "C4: MaxPlus i32 262144x128x128 +argmax",
+    "C5": "C5: MaxPlus f32 4096^3 +argmax forward, then grad_A and grad_B backward",
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
@@ -53,11 +54,12 @@ KERNEL_NAMES = {
     "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
     "C4": "tg_gemm_dl<MaxPlus, i32, argmax>",
+    "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md).  Configs not profiled: None.
-TRAFFIC = {"P": 2.746e9}
+TRAFFIC = {"P": 1.946e9}
 
 
 def cpu_model() -> str:
@@ -100,7 +102,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4"])
+    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4", "C5"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -137,10 +139,25 @@ def main() -> int:
     p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     sr = nat.SEMIRING[cfg["semiring"]]
 
-    def step():
+    backward = cfg.get("backward", False)
+    if backward:
+        g = workloads.make_grad(args.config, m, n, dev, tdt)
+        ga = torch.empty((m, k), dtype=tdt, device=dev)
+        gb = torch.empty((k, n), dtype=tdt, device=dev)
+
+    def forward():
         rc = lib.tg_gemm_ws(0, sr, dt, 0, p(a), p(b), p(c), p(am), m, n, k, p(ws), ws_bytes, s_ptr)
         if rc != 0:
             raise nat.HipError(rc, nat.last_error())
+
+    def backward_only():
+        nat.check(lib.tg_backward_a(0, dt, 0, p(g), p(am), p(ga), m, n, k, s_ptr))
+        nat.check(lib.tg_backward_b(0, dt, 0, p(g), p(am), p(gb), m, n, k, s_ptr))
+
+    def step():
+        forward()
+        if backward:
+            backward_only()
 
     for _ in range(args.warmup):
         step()
@@ -171,6 +188,17 @@ def main() -> int:
     nat.check(lib.tg_kernel_timing_enable(0))
     nat.check(lib.tg_kernel_timing_read(ctypes.byref(tot), ctypes.byref(nl)))
     ms_kernel = tot.value / max(nl.value, 1)
+
+    # C5: the backward pair alone (grad_A, grad_B), timed like the step.
+    ms_backward = None
+    if backward:
+        torch.cuda.synchronize(dev)
+        ev0.record(stream)
+        for _ in range(args.steps):
+            backward_only()
+        ev1.record(stream)
+        torch.cuda.synchronize(dev)
+        ms_backward = ev0.elapsed_time(ev1) / args.steps
 
     # Post-timing sanity check (outside the timed region): every output equals
     # the product at its argmax, bit-exactly.
@@ -225,6 +253,13 @@ def main() -> int:
         "argmax_consistency_check": check,
         "device": torch.cuda.get_device_name(dev),
     }
+    if backward:
+        # Backward bytes: read dC and argmax (4 B each per output), write
+        # grad_A and grad_B once.
+        bwd_bytes = 8 * m * n + esize * (m * k + k * n)
+        out["backward"] = {"ms": round(ms_backward, 4), "algorithmic_bytes": bwd_bytes,
+                           "GB_per_s": round(bwd_bytes / (ms_backward / 1e3) / 1e9, 1),
+                           "frac_of_hbm_peak": round(bwd_bytes / (ms_backward / 1e3) / 8e12, 4)}
     if args.copy_mib > 0:
         src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
