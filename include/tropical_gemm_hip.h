@@ -118,7 +118,9 @@ int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
             int64_t m, int64_t n, int64_t k, void* stream);
 
 /* Bytes of device workspace tg_gemm_ws needs for this problem (0 for
- * value-only).  batch = 1 for single products. */
+ * value-only): B^T staging, batch x k x max(m, n) elements (column-major
+ * calls swap the operands, so the bound covers both layouts).  batch = 1 for
+ * single products. */
 size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,
                               int with_argmax);
 

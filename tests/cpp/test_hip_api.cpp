@@ -54,6 +54,25 @@ static void expect_error(ErrorKind kind, const std::string& needle, F f, int lin
 }
 #define EXPECT_ERROR(kind, needle, body) expect_error(kind, needle, [&] { body; }, __LINE__)
 
+// Element-wise equality that prints the first differences when it fails.
+template <typename T, typename U>
+static bool same_elems(const char* what, const std::vector<T>& got, const std::vector<U>& want) {
+    if (got.size() != want.size()) {
+        std::fprintf(stderr, "%s: size %zu != %zu\n", what, got.size(), want.size());
+        return false;
+    }
+    int shown = 0;
+    size_t bad = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        if (got[i] == T(want[i])) continue;
+        ++bad;
+        if (shown++ < 5)
+            std::fprintf(stderr, "%s: [%zu] got %g want %g\n", what, i, double(got[i]), double(want[i]));
+    }
+    if (bad) std::fprintf(stderr, "%s: %zu of %zu differ\n", what, bad, got.size());
+    return bad == 0;
+}
+
 // ---------------------------------------------------------------------------
 // CPU-only checks
 // ---------------------------------------------------------------------------
@@ -311,7 +330,11 @@ static void gpu_checks() {
         bs.push_back(GpuMat<S>::from_slice(ctx, bv, k, n));
         bs.push_back(GpuMat<S>::from_slice(ctx, bv, k, n));
         auto outs = GpuMat<S>::matmul_batched_with_argmax(ctx, as, bs);
-        CHECK(outs.size() == 2 && outs[1].to_argmax(ctx) == ref.second);
+        CHECK(outs.size() == 2);
+        for (size_t t = 0; t < outs.size(); ++t) {
+            CHECK(same_elems("batched argmax", outs[t].to_argmax(ctx), ref.second));
+            CHECK(same_elems("batched values", outs[t].to_mat(ctx).as_slice(), ref.first));
+        }
         auto mats = GpuMat<S>::to_mats(ctx, GpuMat<S>::matmul_batched(ctx, as, bs));
         CHECK(mats.size() == 2 && mats[0].as_slice() == ref.first);
         CHECK(GpuMat<S>::from_mats(ctx, mats).size() == 2);

@@ -412,3 +412,129 @@ def test_wide_tile_argmax_batched():
     c, am = c.cpu().numpy(), am.cpu().numpy()
     for t in range(12):
         assert_exact(c[t], am[t], *oracle.gemm("minplus", a[t], b[t]))
+
+
+# Argmax problems with K in {64, 96, 128} and full 64 x 64 tiles take the
+# K-resident kernel (whole K panel in LDS, argmax resolved from LDS).
+KRES_SHAPES = [(64, 64, 64), (128, 96, 192), (256, 128, 128), (192, 128, 320)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_k_resident_argmax(sr, dt):
+    rng = np.random.default_rng(500 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in KRES_SHAPES:
+        print(f"[case] k-resident {sr} {dt} m={m} k={k} n={n}", flush=True)
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+        # Heavy ties: values in {0,1,2} put equal maxima in many chunks.
+        a = rng.integers(0, 3, size=(m, k)).astype(dtype)
+        b = rng.integers(0, 3, size=(k, n)).astype(dtype)
+        for api in ("alloc", "ws"):
+            assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
+
+
+def test_k_resident_viterbi_shape_and_batches():
+    from tropical_gemm import ops
+
+    rng = np.random.default_rng(51)
+    # Viterbi-like: emission scores in [-1000, 1000], transitions in [-50, 0].
+    a = rng.integers(-1000, 1001, size=(4096, 128)).astype(np.int32)
+    b = rng.integers(-50, 1, size=(128, 128)).astype(np.int32)
+    c, am = gpu_gemm("maxplus", a, b, True)
+    assert_exact(c, am, *oracle.gemm("maxplus", a, b))
+    # Column-major storage maps onto the same kernel with the operands swapped.
+    c, am = gpu_gemm("maxplus", a[:128], b, True, layout="col")
+    assert_exact(c, am, *oracle.gemm("maxplus", a[:128], b))
+    a3 = rng.standard_normal((5, 128, 64)).astype(np.float32)
+    b3 = rng.standard_normal((5, 64, 192)).astype(np.float32)
+    c3, am3 = ops.gemm_batched("minplus", _dev(a3), _dev(b3), True)
+    c3, am3 = c3.cpu().numpy(), am3.cpu().numpy()
+    for t in range(5):
+        assert_exact(c3[t], am3[t], *oracle.gemm("minplus", a3[t], b3[t]))
+
+
+def test_k_resident_special_values():
+    rng = np.random.default_rng(52)
+    a = rng.standard_normal((128, 128)).astype(np.float32)
+    b = rng.standard_normal((128, 64)).astype(np.float32)
+    a[rng.random(a.shape) < 0.3] = np.inf
+    b[rng.random(b.shape) < 0.3] = np.inf
+    a[7, :] = np.inf  # row never beats the MinPlus zero: +inf, argmax 0
+    c, am = gpu_gemm("minplus", a, b)
+    assert_exact(c, am, *oracle.gemm("minplus", a, b))
+    assert np.all(np.isposinf(c[7])) and np.all(am[7] == 0)
+    # MaxMul: products <= 0 never beat the zero.
+    a3 = rng.integers(-2, 3, size=(64, 64)).astype(np.float32)
+    b3 = rng.integers(-2, 3, size=(64, 64)).astype(np.float32)
+    assert_exact(*gpu_gemm("maxmul", a3, b3), *oracle.gemm("maxmul", a3, b3))
+    # Signed zeros: -0 at k=0 ties +0 later in the same and in later chunks.
+    z = np.zeros((64, 96), np.float32)
+    z[:, 0] = -0.0
+    bz = np.full((96, 64), -1.0, np.float32)
+    bz[0, :] = -0.0
+    bz[3, :] = 0.0
+    bz[70, :] = 0.0
+    c, am = gpu_gemm("maxplus", z, bz)
+    assert_exact(c, am, *oracle.gemm("maxplus", z, bz))
+    assert np.all(np.signbit(c)) and np.all(am == 0)
+
+
+# The B^T workspace: exactly tg_gemm_workspace_size bytes must suffice for
+# both layouts (column-major calls swap the operands, so the kernel's B is A
+# and needs k x m elements).  A guard region after the workspace must be left
+# untouched.
+@pytest.mark.parametrize("layout", ["row", "col"])
+@pytest.mark.parametrize("shape", [(45, 77, 29), (29, 77, 45), (130, 64, 64), (64, 64, 130),
+                                   (256, 96, 128)])
+def test_workspace_bound_and_guard(layout, shape):
+    nat = _nat()
+    lib = nat.load()
+    m, k, n = shape
+    rng = np.random.default_rng(61)
+    a = rng.integers(-20, 21, size=(m, k)).astype(np.float32)
+    b = rng.integers(-20, 21, size=(k, n)).astype(np.float32)
+    c_ref, am_ref = oracle.gemm("maxplus", a, b)
+    if layout == "col":
+        ta, tb = _dev(np.asfortranarray(a).T.copy()), _dev(np.asfortranarray(b).T.copy())
+    else:
+        ta, tb = _dev(a), _dev(b)
+    ws_bytes = lib.tg_gemm_workspace_size(0, 1, m, n, k, 1)
+    assert ws_bytes >= k * max(m, n) * 4
+    guard = 65536
+    ws = torch.full((ws_bytes + guard,), 0xA5, dtype=torch.uint8, device=DEV)
+    c = torch.empty(m * n, dtype=torch.float32, device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.check(lib.tg_gemm_ws(0, 0, 0, nat.LAYOUT[layout], _p(ta), _p(tb), _p(c), _p(am), m, n, k,
+                             _p(ws), ws_bytes, stream))
+    torch.cuda.synchronize()
+    assert bool(torch.all(ws[ws_bytes:] == 0xA5)), "workspace overrun"
+    if layout == "col":
+        c_np, am_np = c.cpu().numpy().reshape(n, m).T, am.cpu().numpy().reshape(n, m).T
+    else:
+        c_np, am_np = c.cpu().numpy().reshape(m, n), am.cpu().numpy().reshape(m, n)
+    assert_exact(c_np, am_np, c_ref, am_ref)
+    # Strided batches of the same product: the workspace holds one B^T each.
+    batch = 3
+    ta3 = ta.reshape(-1).repeat(batch)
+    tb3 = tb.reshape(-1).repeat(batch)
+    ws_bytes = lib.tg_gemm_workspace_size(0, batch, m, n, k, 1)
+    ws = torch.full((ws_bytes + guard,), 0xA5, dtype=torch.uint8, device=DEV)
+    c3 = torch.empty(batch * m * n, dtype=torch.float32, device=DEV)
+    am3 = torch.empty(batch * m * n, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm_strided_batched_ws(0, 0, 0, nat.LAYOUT[layout], _p(ta3), _p(tb3), _p(c3),
+                                             _p(am3), batch, m, n, k, m * k, k * n, m * n, _p(ws),
+                                             ws_bytes, stream))
+    torch.cuda.synchronize()
+    assert bool(torch.all(ws[ws_bytes:] == 0xA5)), "batched workspace overrun"
+    for t in range(batch):
+        ct = c3[t * m * n:(t + 1) * m * n].cpu().numpy()
+        at = am3[t * m * n:(t + 1) * m * n].cpu().numpy()
+        if layout == "col":
+            ct, at = ct.reshape(n, m).T, at.reshape(n, m).T
+        else:
+            ct, at = ct.reshape(m, n), at.reshape(m, n)
+        assert_exact(ct, at, c_ref, am_ref)

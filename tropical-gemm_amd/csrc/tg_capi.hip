@@ -16,6 +16,7 @@
 
 #include "../../include/tropical_gemm_hip.h"
 #include "tg_gemm_dl.hpp"
+#include "tg_gemm_kres.hpp"
 #include "tg_kernels.hpp"
 
 namespace {
@@ -214,9 +215,60 @@ int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
     return TG_OK;
 }
 
+// K-resident argmax kernel for short K (32-bit types): no B^T staging.
+template <int SR, typename T>
+int run_gemm_kres(const Problem& p, hipStream_t st) {
+    using Cfg = tg::KresCfg;
+    const int64_t tiles_m = p.M / Cfg::BM;
+    const int64_t tiles_n = p.N / Cfg::BN;
+    if (tiles_m * tiles_n > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    const T* A = static_cast<const T*>(p.A);
+    const T* B = static_cast<const T*>(p.B);
+    T* C = static_cast<T*>(p.C);
+    const int kt = int(p.K / Cfg::BK);
+    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+        const T* Az = A + z0 * p.sA;
+        const T* Bz = B + z0 * p.sB;
+        T* Cz = C + z0 * p.sC;
+        int32_t* Iz = p.IDX + z0 * p.sC;
+        dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+        KernelTimer timer(st);
+        switch (kt) {
+            case 2:
+                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 2>), grid, dim3(256), 0, st, Az, Bz, Cz,
+                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+                break;
+            case 3:
+                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 3>), grid, dim3(256), 0, st, Az, Bz, Cz,
+                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+                break;
+            case 4:
+                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 4>), grid, dim3(256), 0, st, Az, Bz, Cz,
+                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+                break;
+            default:
+                return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
+        }
+        TG_HIP(hipGetLastError());
+    }
+    return TG_OK;
+}
+
+// True when the argmax problem runs on the K-resident kernel (which needs no
+// B^T workspace).
+bool uses_kres(tg_dtype dt, const Problem& p) {
+    return (dt == TG_F32 || dt == TG_I32) && p.IDX != nullptr &&
+           tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX);
+}
+
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
     if constexpr (sizeof(T) == 4) {
+        if (p.IDX != nullptr &&
+            tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_kres<SR, T>(p, st);
         // Argmax chunk length: bookkeeping costs ~3 ops per output per chunk
         // (3K/CL) and the exact resolve ~4 ops per product of one chunk
         // (4*CL); the sum is smallest near CL = sqrt(3K/4).
@@ -317,11 +369,15 @@ int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, hipStream_
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// B^T staging for argmax problems: K x N' elements per batch item, where N'
+// is the kernel's N after the layout mapping (n for row-major calls, m for
+// column-major ones, whose operands are swapped).  The size does not depend
+// on the layout: K x max(m, n) covers both.
 size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
                            bool with_argmax) {
-    (void)m;
-    if (!with_argmax || batch <= 0 || n <= 0 || k <= 0) return 0;
-    return round_up(size_t(batch) * size_t(k) * size_t(n) * size_t(elem_size(dt)), 256);
+    if (!with_argmax || batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
+    const int64_t wide = m > n ? m : n;
+    return round_up(size_t(batch) * size_t(k) * size_t(wide) * size_t(elem_size(dt)), 256);
 }
 
 // Validation shared by the forward entry points.  Returns TG_OK or an error.
@@ -387,9 +443,12 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
         p.sC = p.M * p.N;
     }
 
+    // The kernels stage B^T (K x p.N per batch item) in the workspace.
+    if (need > 0 && need < size_t(p.batch) * size_t(p.K) * size_t(p.N) * size_t(elem_size(dt)))
+        return fail(TG_ERR_INVALID_ARGUMENT, "internal: workspace size below K x N");
     void* work = ws;
     bool own = false;
-    if (need > 0 && !ws_given) {
+    if (need > 0 && !ws_given && !uses_kres(dt, p)) {
         TG_HIP(hipMallocAsync(&work, need, st));
         own = true;
     }

@@ -198,22 +198,21 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         __syncthreads();
         if (t + 1 < ntiles) issue_loads(t + 1, buf ^ 1);
 
-        // The LDS tile holds BK / CL argmax chunks of CL consecutive k.
+        // The LDS tile holds BK / CL argmax chunks of CL consecutive k.  Each
+        // chunk folds its products into a max3/min3 chain that starts from
+        // the running value, so the running value needs no separate update;
+        // with argmax the chunk is recorded iff the chain's result beats the
+        // value held before the chunk strictly (the reference's "keep acc iff
+        // acc >= p").
 #pragma unroll
         for (int s = 0; s < BK / CL; ++s) {
-            T cm[TM][TN];
-            {
-                T a[TM][2], b[2][TN];
-                load_frag(buf, s * CL, a, b);
+            T an[TM][TN];
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a[i][0], b[0][j]),
-                                                tmul<SR, T>(a[i][1], b[1][j]));
-            }
+                for (int j = 0; j < TN; ++j) an[i][j] = acc[i][j];
 #pragma unroll
-            for (int kk = s * CL + 2; kk < (s + 1) * CL; kk += 2) {
+            for (int kk = s * CL; kk < (s + 1) * CL; kk += 2) {
                 T a[TM][2], b[2][TN];
                 load_frag(buf, kk, a, b);
 #pragma unroll
@@ -222,19 +221,18 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                     for (int j = 0; j < TN; ++j) {
                         const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
                         const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
-                        cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
+                        an[i][j] = tjoin<SR, T>(tjoin<SR, T>(an[i][j], p0), p1);
                     }
             }
-            // Strict improvement only (the reference's "keep acc iff acc >= p").
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     if constexpr (ARGMAX) {
-                        if (tbetter<SR, T>(cm[i][j], acc[i][j]))
+                        if (tbetter<SR, T>(an[i][j], acc[i][j]))
                             ch[i][j] = int32_t(t * (BK / CL) + s);
                     }
-                    acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
+                    acc[i][j] = an[i][j];
                 }
         }
     }
