@@ -538,3 +538,35 @@ def test_workspace_bound_and_guard(layout, shape):
         else:
             ct, at = ct.reshape(m, n), at.reshape(m, n)
         assert_exact(ct, at, c_ref, am_ref)
+
+
+# The K-resident kernel's three i32 paths, chosen per workgroup from the
+# magnitudes in its panels: f32 keys (all |x| < 2^15), i32 keys (< 2^22) and
+# the chunked path (anything larger, including wraparound).
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+def test_k_resident_integer_paths(sr):
+    rng = np.random.default_rng(53)
+    m, k, n = 256, 128, 128
+    cases = {
+        "f32-key boundary": (rng.choice([-32768, -32767, 0, 32766, 32767], size=(m, k)),
+                             rng.choice([-32768, 32767, 1, -1], size=(k, n))),
+        "i32-key": (rng.integers(-(1 << 21), 1 << 21, size=(m, k)),
+                    rng.integers(-(1 << 21), 1 << 21, size=(k, n))),
+        "i32-key ties": (rng.integers(0, 3, size=(m, k)) * 40000,
+                         rng.integers(0, 3, size=(k, n)) * 40000),
+        "chunked wraparound": (rng.integers(2**31 - 60, 2**31 - 1, size=(m, k)),
+                               rng.integers(-5, 60, size=(k, n))),
+    }
+    for name, (a, b) in cases.items():
+        print(f"[case] k-resident {sr} i32 {name}", flush=True)
+        a = a.astype(np.int32)
+        b = b.astype(np.int32)
+        assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+    # One workgroup's panel (rows 64..127) holds a large value: that workgroup
+    # takes the chunked path, the others keep the key paths.
+    a = rng.integers(-1000, 1001, size=(m, k)).astype(np.int32)
+    b = rng.integers(-50, 1, size=(k, n)).astype(np.int32)
+    a[100, 7] = 1 << 24
+    assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+    a[100, 7] = 1 << 17
+    assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
