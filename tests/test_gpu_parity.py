@@ -570,3 +570,96 @@ def test_k_resident_integer_paths(sr):
     assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
     a[100, 7] = 1 << 17
     assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+
+
+# Split K: full-tile 32-bit problems with few 64 x 64 tiles run K in slices
+# (up to 1024 workgroups, slices of >= 256 k) and merge the per-slice
+# (value, first k) partials; ties go to the earlier slice.
+SPLIT_SHAPES = [(64, 4096, 64), (128, 512, 128), (256, 8192, 256), (192, 1536, 320)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_split_k(sr, dt):
+    nat = _nat()
+    lib = nat.load()
+    rng = np.random.default_rng(600 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n) in SPLIT_SHAPES:
+        full = lib.tg_gemm_workspace_size(nat.DTYPE[dt], 1, m, n, k, 1)
+        assert full > k * max(m, n) * 4, "split-K partials must be part of the workspace size"
+        print(f"[case] split-k {sr} {dt} m={m} k={k} n={n}", flush=True)
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        c_ref, am_ref = oracle.gemm(sr, a, b)
+        for api in ("alloc", "ws"):
+            assert_exact(*gpu_gemm(sr, a, b, True, api=api), c_ref, am_ref)
+            c, _ = gpu_gemm(sr, a, b, False, api=api)
+            assert_exact(c, None, c_ref, None)
+        # Equal maxima in many slices: the first k must win.
+        a = rng.integers(0, 3, size=(m, k)).astype(dtype)
+        b = rng.integers(0, 3, size=(k, n)).astype(dtype)
+        assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+
+
+def test_split_k_signed_zero_and_infinities():
+    # -0 at k = 0 (slice 0) ties +0 at k = 3000 (a later slice): -0 / index 0.
+    m, k, n = 64, 4096, 64
+    a = np.zeros((m, k), np.float32)
+    a[:, 0] = -0.0
+    b = np.full((k, n), -1.0, np.float32)
+    b[0, :] = -0.0
+    b[3000, :] = 0.0
+    c, am = gpu_gemm("maxplus", a, b)
+    assert_exact(c, am, *oracle.gemm("maxplus", a, b))
+    assert np.all(np.signbit(c)) and np.all(am == 0)
+    # +inf entries (MinPlus "no edge") with rows that are +inf in every slice.
+    rng = np.random.default_rng(62)
+    a = (rng.random((m, k)) * 100).astype(np.float32)
+    b = (rng.random((k, n)) * 100).astype(np.float32)
+    a[rng.random(a.shape) < 0.3] = np.inf
+    b[rng.random(b.shape) < 0.3] = np.inf
+    a[5, :] = np.inf
+    c, am = gpu_gemm("minplus", a, b)
+    assert_exact(c, am, *oracle.gemm("minplus", a, b))
+    assert np.all(np.isposinf(c[5])) and np.all(am[5] == 0)
+
+
+def test_split_k_minimum_workspace_and_batches():
+    nat = _nat()
+    lib = nat.load()
+    rng = np.random.default_rng(63)
+    m, k, n = 128, 2048, 128
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    c_ref, am_ref = oracle.gemm("maxplus", a, b)
+    # A workspace of just the B^T staging runs the product unsplit.
+    ws_min = k * n * 4
+    ws = torch.empty(ws_min, dtype=torch.uint8, device=DEV)
+    ta, tb = _dev(a), _dev(b)
+    c = torch.empty(m * n, dtype=torch.float32, device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm_ws(0, 0, 0, 0, _p(ta), _p(tb), _p(c), _p(am), m, n, k, _p(ws), ws_min,
+                             None))
+    torch.cuda.synchronize()
+    assert_exact(c.cpu().numpy().reshape(m, n), am.cpu().numpy().reshape(m, n), c_ref, am_ref)
+    # Strided batches with gaps between the outputs, split as one problem.
+    from tropical_gemm import ops
+
+    a3 = rng.standard_normal((3, 128, 1024)).astype(np.float32)
+    b3 = rng.standard_normal((3, 1024, 64)).astype(np.float32)
+    c3, am3 = ops.gemm_batched("maxplus", _dev(a3), _dev(b3), True)
+    c3, am3 = c3.cpu().numpy(), am3.cpu().numpy()
+    for t in range(3):
+        assert_exact(c3[t], am3[t], *oracle.gemm("maxplus", a3[t], b3[t]))
+    batch, sc = 3, 128 * 64 + 64
+    ta3, tb3 = _dev(a3), _dev(b3)
+    cc = torch.zeros(batch * sc, dtype=torch.float32, device=DEV)
+    aa = torch.zeros(batch * sc, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm_strided_batched(0, 0, 0, 0, _p(ta3), _p(tb3), _p(cc), _p(aa), batch, 128,
+                                          64, 1024, 128 * 1024, 1024 * 64, sc, None))
+    torch.cuda.synchronize()
+    cc, aa = cc.cpu().numpy(), aa.cpu().numpy()
+    for t in range(batch):
+        assert_exact(cc[t * sc: t * sc + 128 * 64].reshape(128, 64),
+                     aa[t * sc: t * sc + 128 * 64].reshape(128, 64), *oracle.gemm("maxplus", a3[t], b3[t]))

@@ -174,9 +174,31 @@ struct Problem {
     int64_t batch, M, N, K, sA, sB, sC;
 };
 
-// Direct-to-LDS kernel for 32-bit types when every tile is full.
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Workspace layout: [B^T staging (argmax)][split-K value partials][split-K
+// index partials (argmax)], each region 256-byte aligned.
+struct WsLayout {
+    size_t bt = 0, pv = 0, pi = 0, total = 0;
+};
+
+WsLayout ws_layout(tg_dtype dt, int64_t batch, int64_t M, int64_t N, int64_t K, bool argmax,
+                   int splits) {
+    WsLayout w;
+    const size_t es = size_t(elem_size(dt));
+    const size_t bt = argmax ? round_up(size_t(batch) * size_t(K) * size_t(N) * es, 256) : 0;
+    const size_t part = splits > 1 ? round_up(size_t(splits) * size_t(batch) * size_t(M) * size_t(N) * es, 256) : 0;
+    w.bt = 0;
+    w.pv = bt;
+    w.pi = bt + part;
+    w.total = bt + part + (argmax ? part : 0);
+    return w;
+}
+
+// Direct-to-LDS kernel for 32-bit types when every tile is full.  splits > 1
+// runs K in that many slices into the workspace partials, then merges them.
 template <int SR, typename T, int TN, int CL>
-int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
+int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     using Cfg = tg::DlCfg<TN>;
     const int64_t tiles_m = p.M / Cfg::BM;
     const int64_t tiles_n = p.N / Cfg::BN;
@@ -186,30 +208,58 @@ int run_gemm_dl(const Problem& p, void* ws, hipStream_t st) {
     const T* B = static_cast<const T*>(p.B);
     T* C = static_cast<T*>(p.C);
     const bool argmax = p.IDX != nullptr;
+    const WsLayout wl = ws_layout(std::is_same<T, float>::value ? TG_F32 : TG_I32, p.batch, p.M,
+                                  p.N, p.K, argmax, splits);
+    unsigned char* wsb = static_cast<unsigned char*>(ws);
+    T* PV = splits > 1 ? reinterpret_cast<T*>(wsb + wl.pv) : nullptr;
+    int32_t* PI = (splits > 1 && argmax) ? reinterpret_cast<int32_t*>(wsb + wl.pi) : nullptr;
+    const int64_t MN = p.M * p.N;
+    const int64_t sY = splits > 1 ? p.batch * MN : 0;
+    const int64_t KS = p.K / splits;
+    if (argmax) {  // B^T staging for the resolve, outside the timed GEMM launches
+        if ((p.K + 31) / 32 > 65535)
+            return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
+        for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+            const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+            T* BT = reinterpret_cast<T*>(wsb + wl.bt) + z0 * p.K * p.N;
+            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+            hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB, BT,
+                               p.K, p.N, p.sB, p.K * p.N);
+            TG_HIP(hipGetLastError());
+        }
+    }
+    KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
         const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
         const T* Az = A + z0 * p.sA;
         const T* Bz = B + z0 * p.sB;
-        T* Cz = C + z0 * p.sC;
-        dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+        // Split launches write dense partials (batch stride M*N).
+        T* Cz = splits > 1 ? PV + z0 * MN : C + z0 * p.sC;
+        int32_t* Iz = !argmax ? nullptr : splits > 1 ? PI + z0 * MN : p.IDX + z0 * p.sC;
+        const int64_t sCk = splits > 1 ? MN : p.sC;
+        dim3 grid(unsigned(tiles_m * tiles_n), unsigned(splits), unsigned(nb));
         if (argmax) {
-            T* BT = static_cast<T*>(ws);
-            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
-            if ((p.K + 31) / 32 > 65535)
-                return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
-            hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, Bz, BT, p.K, p.N,
-                               p.sB, p.K * p.N);
-            TG_HIP(hipGetLastError());
-            KernelTimer timer(st);
+            const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
             hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
-                               Az, Bz, BT, Cz, p.IDX + z0 * p.sC, p.M, p.N, p.K, p.sA, p.sB, p.sC,
-                               int(tiles_m), int(tiles_n));
+                               Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, sCk,
+                               int(tiles_m), int(tiles_n), KS, sY);
         } else {
-            KernelTimer timer(st);
             hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
-                               Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, p.sC,
-                               int(tiles_m), int(tiles_n));
+                               Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, sCk,
+                               int(tiles_m), int(tiles_n), KS, sY);
         }
+        TG_HIP(hipGetLastError());
+    }
+    if (splits > 1) {
+        const int64_t nvec = p.batch * MN / 4;
+        int64_t blocks = (nvec + 255) / 256;
+        if (blocks > 8192) blocks = 8192;
+        if (argmax)
+            hipLaunchKernelGGL((tg::tg_merge_splits<SR, T, true>), dim3(unsigned(blocks)), dim3(256), 0,
+                               st, PV, PI, C, p.IDX, splits, MN, p.batch, sY, p.sC);
+        else
+            hipLaunchKernelGGL((tg::tg_merge_splits<SR, T, false>), dim3(unsigned(blocks)), dim3(256), 0,
+                               st, PV, nullptr, C, nullptr, splits, MN, p.batch, sY, p.sC);
         TG_HIP(hipGetLastError());
     }
     return TG_OK;
@@ -264,30 +314,37 @@ bool uses_kres(tg_dtype dt, const Problem& p) {
 }
 
 template <int SR, typename T>
-int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
+int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
     if constexpr (sizeof(T) == 4) {
         if (p.IDX != nullptr &&
             tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
             return run_gemm_kres<SR, T>(p, st);
-        // Argmax chunk length: bookkeeping costs ~3 ops per output per chunk
-        // (3K/CL) and the exact resolve ~4 ops per product of one chunk
-        // (4*CL); the sum is smallest near CL = sqrt(3K/4).
         const bool argmax = p.IDX != nullptr;
-        const int cl = !argmax ? 32 : p.K <= 192 ? 8 : p.K <= 768 ? 16 : 32;
+        const tg_dtype dt = std::is_same<T, float>::value ? TG_F32 : TG_I32;
+        // Split K when the problem makes too few 64 x 64 tiles and the
+        // workspace holds the partials (tg_gemm_workspace_size includes them).
+        int splits = tg::dl_splits(p.M, p.N, p.K, p.batch);
+        if (splits > 1 && ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, splits).total > ws_bytes)
+            splits = 1;
+        const int64_t ks = p.K / splits;
+        // Argmax chunk length: bookkeeping costs ~2 ops per output per chunk
+        // (2K/CL) and the exact resolve ~4 ops per product of one chunk
+        // (4*CL per slice); the sum is smallest near CL = sqrt(K/2) per slice.
+        const int cl = !argmax ? 32 : ks <= 192 ? 8 : ks <= 768 ? 16 : 32;
         // 64 x 128 tiles for argmax problems big enough that the last round
         // of 768 resident workgroups is a small share of the work (their
         // main loop is the faster one); 64 x 64 tiles otherwise (value-only
         // runs four workgroups per CU, small problems get twice the tiles).
-        const bool wide = argmax && cl == 32 && p.N % tg::DlCfg<8>::BN == 0 &&
+        const bool wide = splits == 1 && argmax && cl == 32 && p.N % tg::DlCfg<8>::BN == 0 &&
                           (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
         if (wide && tg::dl_fits<8, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 8, 32>(p, ws, st);
+            return run_gemm_dl<SR, T, 8, 32>(p, ws, 1, st);
         if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 8>(p, ws, st);
+            return run_gemm_dl<SR, T, 4, 8>(p, ws, splits, st);
         if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 16>(p, ws, st);
+            return run_gemm_dl<SR, T, 4, 16>(p, ws, splits, st);
         if (cl == 32 && tg::dl_fits<4, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 32>(p, ws, st);
+            return run_gemm_dl<SR, T, 4, 32>(p, ws, splits, st);
     }
     using Cfg = tg::TileCfg<T>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
@@ -348,36 +405,52 @@ int run_gemm_typed(const Problem& p, void* ws, hipStream_t st) {
 }
 
 template <int SR>
-int run_gemm_sr(tg_dtype dt, const Problem& p, void* ws, hipStream_t st) {
+int run_gemm_sr(tg_dtype dt, const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
     switch (dt) {
-        case TG_F32: return run_gemm_typed<SR, float>(p, ws, st);
-        case TG_F64: return run_gemm_typed<SR, double>(p, ws, st);
-        case TG_I32: return run_gemm_typed<SR, int32_t>(p, ws, st);
-        case TG_I64: return run_gemm_typed<SR, int64_t>(p, ws, st);
+        case TG_F32: return run_gemm_typed<SR, float>(p, ws, ws_bytes, st);
+        case TG_F64: return run_gemm_typed<SR, double>(p, ws, ws_bytes, st);
+        case TG_I32: return run_gemm_typed<SR, int32_t>(p, ws, ws_bytes, st);
+        case TG_I64: return run_gemm_typed<SR, int64_t>(p, ws, ws_bytes, st);
     }
     return fail(TG_ERR_INVALID_ARGUMENT, "bad dtype");
 }
 
-int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, hipStream_t st) {
+int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, size_t ws_bytes,
+             hipStream_t st) {
     switch (sr) {
-        case TG_MAXPLUS: return run_gemm_sr<tg::SR_MAXPLUS>(dt, p, ws, st);
-        case TG_MINPLUS: return run_gemm_sr<tg::SR_MINPLUS>(dt, p, ws, st);
-        case TG_MAXMUL: return run_gemm_sr<tg::SR_MAXMUL>(dt, p, ws, st);
+        case TG_MAXPLUS: return run_gemm_sr<tg::SR_MAXPLUS>(dt, p, ws, ws_bytes, st);
+        case TG_MINPLUS: return run_gemm_sr<tg::SR_MINPLUS>(dt, p, ws, ws_bytes, st);
+        case TG_MAXMUL: return run_gemm_sr<tg::SR_MAXMUL>(dt, p, ws, ws_bytes, st);
     }
     return fail(TG_ERR_INVALID_ARGUMENT, "bad semiring");
 }
 
-size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
 // B^T staging for argmax problems: K x N' elements per batch item, where N'
 // is the kernel's N after the layout mapping (n for row-major calls, m for
 // column-major ones, whose operands are swapped).  The size does not depend
-// on the layout: K x max(m, n) covers both.
-size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
-                           bool with_argmax) {
+// on the layout: K x max(m, n) covers both.  This is the minimum workspace.
+size_t bt_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k, bool with_argmax) {
     if (!with_argmax || batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
     const int64_t wide = m > n ? m : n;
     return round_up(size_t(batch) * size_t(k) * size_t(wide) * size_t(elem_size(dt)), 256);
+}
+
+// Full workspace: the minimum plus the split-K partials (values, and indices
+// for argmax) of 32-bit full-tile problems that make too few tiles
+// (tg::dl_splits, symmetric in m and n).  A workspace of at least the minimum
+// runs the same products unsplit.
+size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
+                           bool with_argmax) {
+    if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
+    size_t w = bt_bytes_for(dt, batch, m, n, k, with_argmax);
+    if (elem_size(dt) == 4) {
+        const int s = tg::dl_splits(m, n, k, batch);
+        if (s > 1) {
+            const size_t part = round_up(size_t(s) * size_t(batch) * size_t(m) * size_t(n) * 4, 256);
+            w += part * (with_argmax ? 2 : 1);
+        }
+    }
+    return w;
 }
 
 // Validation shared by the forward entry points.  Returns TG_OK or an error.
@@ -416,7 +489,7 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
     int rc = validate_forward(sr, dt, layout, A, B, C, batch, m, n, k, sa, sb, sc, strided);
     if (rc != TG_OK) return rc;
     const bool with_argmax = argmax != nullptr;
-    const size_t need = workspace_bytes_for(dt, batch, m, n, k, with_argmax);
+    const size_t need = bt_bytes_for(dt, batch, m, n, k, with_argmax);
     if (ws_given && need > 0) {
         if (ws == nullptr || ws_bytes < need)
             return fail(TG_ERR_INVALID_ARGUMENT, "workspace too small: need " + std::to_string(need) +
@@ -424,6 +497,9 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
         if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
             return fail(TG_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
+    // A workspace the split-K partials cannot use (none, or misaligned when
+    // no B^T staging is needed) runs the product unsplit.
+    if (ws_given && (ws == nullptr || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)) ws_bytes = 0;
     rc = select_device(device);
     if (rc != TG_OK) return rc;
     if (batch == 0 || m == 0 || n == 0) return TG_OK;
@@ -448,11 +524,14 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
         return fail(TG_ERR_INVALID_ARGUMENT, "internal: workspace size below K x N");
     void* work = ws;
     bool own = false;
-    if (need > 0 && !ws_given && !uses_kres(dt, p)) {
-        TG_HIP(hipMallocAsync(&work, need, st));
-        own = true;
+    if (!ws_given && !uses_kres(dt, p)) {
+        ws_bytes = workspace_bytes_for(dt, batch, m, n, k, with_argmax);
+        if (ws_bytes > 0) {
+            TG_HIP(hipMallocAsync(&work, ws_bytes, st));
+            own = true;
+        }
     }
-    rc = run_gemm(sr, dt, p, work, st);
+    rc = run_gemm(sr, dt, p, work, ws_given || own ? ws_bytes : 0, st);
     if (own) {
         hipError_t e = hipFreeAsync(work, st);
         if (rc == TG_OK && e != hipSuccess) return hip_fail(e, "hipFreeAsync");

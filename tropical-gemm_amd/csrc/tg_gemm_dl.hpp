@@ -98,6 +98,55 @@ inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int
            sC % 4 == 0 && a16(A) && a16(B) && a16(C) && (IDX == nullptr || a16(IDX));
 }
 
+// Split K for full-tile problems with too few 64 x 64 tiles to fill the
+// chip: the largest power of two S with at most 1024 workgroups in total,
+// slices of at least 256 k and slice lengths that are multiples of 64.
+inline int dl_splits(int64_t M, int64_t N, int64_t K, int64_t batch) {
+    if (M % 64 != 0 || N % 64 != 0 || K % 64 != 0 || batch <= 0) return 1;
+    const int64_t tiles = (M / 64) * (N / 64) * batch;
+    int s = 1;
+    while (tiles * s * 2 <= 1024 && K % (int64_t(64) * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
+    return s;
+}
+
+// Combines the S split-K partials of tg_gemm_dl.  Slices are visited in k
+// order and a later slice replaces the running result only if strictly
+// better, so equal values keep the earlier slice's index and bits: the
+// reference's first-k rule across slices.  Partials are dense, slice stride
+// sY = batch * M * N; outputs use the batch stride sC.  16-byte vectors
+// (M * N is a multiple of 4096 here).
+template <int SR, typename T, bool ARGMAX>
+__global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
+                                                       const int32_t* __restrict__ PI,
+                                                       T* __restrict__ C, int32_t* __restrict__ IDX,
+                                                       int S, int64_t MN, int64_t batch, int64_t sY,
+                                                       int64_t sC) {
+    const int64_t nvec = batch * MN / 4;
+    const int64_t stride = int64_t(gridDim.x) * 256;
+    for (int64_t v = int64_t(blockIdx.x) * 256 + threadIdx.x; v < nvec; v += stride) {
+        const int64_t e = v * 4;
+        const int64_t z = e / MN;
+        const int64_t r = e - z * MN;
+        Vec16<T> best = *reinterpret_cast<const Vec16<T>*>(PV + e);
+        Vec16<int32_t> bi{};
+        if constexpr (ARGMAX) bi = *reinterpret_cast<const Vec16<int32_t>*>(PI + e);
+        for (int y = 1; y < S; ++y) {
+            const Vec16<T> pv = *reinterpret_cast<const Vec16<T>*>(PV + y * sY + e);
+            Vec16<int32_t> pi{};
+            if constexpr (ARGMAX) pi = *reinterpret_cast<const Vec16<int32_t>*>(PI + y * sY + e);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (tbetter<SR, T>(pv.v[q], best.v[q])) {
+                    best.v[q] = pv.v[q];
+                    if constexpr (ARGMAX) bi.v[q] = pi.v[q];
+                }
+            }
+        }
+        *reinterpret_cast<Vec16<T>*>(C + z * sC + r) = best;
+        if constexpr (ARGMAX) *reinterpret_cast<Vec16<int32_t>*>(IDX + z * sC + r) = bi;
+    }
+}
+
 // Waves per SIMD come from the tile configuration (DlCfg): other resident
 // waves hide the LDS latency of the main loop.
 template <int SR, typename T, bool ARGMAX, int TN_, int CL>
@@ -105,7 +154,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     ARGMAX ? DlCfg<TN_>::WAVES_ARGMAX : DlCfg<TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
-    int64_t sB, int64_t sC, int tiles_m, int tiles_n) {
+    int64_t sB, int64_t sC, int tiles_m, int tiles_n, int64_t KS, int64_t sY) {
     static_assert(sizeof(T) == 4, "direct-to-LDS kernel is for 32-bit types");
     using Cfg = DlCfg<TN_>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, TM = Cfg::TM, TN = Cfg::TN;
@@ -127,9 +176,13 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     const int64_t z = blockIdx.z;
     A += z * sA;
     B += z * sB;
-    C += z * sC;
+    // Split K: slice y covers k in [y*KS, (y+1)*KS) and writes its (value,
+    // argmax) partial at C/IDX + y*sY (tg_merge_splits combines them).  An
+    // unsplit launch has gridDim.y == 1, KS == K and sY == 0.
+    const int64_t y = blockIdx.y;
+    C += z * sC + y * sY;
     if (ARGMAX) {
-        IDX += z * sC;
+        IDX += z * sC + y * sY;
         BT += z * (N * K);
     }
 
@@ -190,13 +243,15 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 b[h][j] = bs[(kk + h) * BN + (j >> 2) * 64 + tx * 4 + (j & 3)];
     };
 
-    const int64_t ntiles = K / BK;
-    issue_loads(0, 0);
-    for (int64_t t = 0; t < ntiles; ++t) {
-        const int buf = int(t & 1);
+    // k-tiles [t0, t1) of this slice; t (and so every chunk index) is global.
+    const int64_t t0 = y * (KS / BK);
+    const int64_t t1 = t0 + KS / BK;
+    issue_loads(t0, 0);
+    for (int64_t t = t0; t < t1; ++t) {
+        const int buf = int((t - t0) & 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (t + 1 < ntiles) issue_loads(t + 1, buf ^ 1);
+        if (t + 1 < t1) issue_loads(t + 1, buf ^ 1);
 
         // The LDS tile holds BK / CL argmax chunks of CL consecutive k.  Each
         // chunk folds its products into a max3/min3 chain that starts from
