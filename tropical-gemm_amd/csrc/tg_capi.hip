@@ -265,44 +265,61 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     return TG_OK;
 }
 
-// K-resident argmax kernel for short K (32-bit types): no B^T staging.
+// Compute units of the current device (cached per device).
+int current_cu_count() {
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    if (int(cache.size()) <= dev) cache.resize(dev + 1, 0);
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+// K-resident argmax kernel for short K (32-bit types): no B^T staging.  A
+// persistent grid of two workgroups per CU (their LDS panels allow two),
+// each owning one column tile.
 template <int SR, typename T>
 int run_gemm_kres(const Problem& p, hipStream_t st) {
     using Cfg = tg::KresCfg;
     const int64_t tiles_m = p.M / Cfg::BM;
     const int64_t tiles_n = p.N / Cfg::BN;
-    if (tiles_m * tiles_n > 0x7fffffffLL)
+    if (tiles_m > 0x7fffffffLL || tiles_n > 0x7fffffffLL)
         return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    const int64_t total = p.batch * tiles_m * tiles_n;
+    int64_t grid = int64_t(2) * current_cu_count();
+    grid = (grid / tiles_n) * tiles_n;
+    if (grid < tiles_n) grid = tiles_n;
+    if (grid > total) grid = total;
+    if (grid > 0x7fffffffLL) return fail(TG_ERR_DIMENSION_MISMATCH, "too many column tiles");
     const T* A = static_cast<const T*>(p.A);
     const T* B = static_cast<const T*>(p.B);
     T* C = static_cast<T*>(p.C);
+    KernelTimer timer(st);
     const int kt = int(p.K / Cfg::BK);
-    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
-        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
-        const T* Az = A + z0 * p.sA;
-        const T* Bz = B + z0 * p.sB;
-        T* Cz = C + z0 * p.sC;
-        int32_t* Iz = p.IDX + z0 * p.sC;
-        dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
-        KernelTimer timer(st);
-        switch (kt) {
-            case 2:
-                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 2>), grid, dim3(256), 0, st, Az, Bz, Cz,
-                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
-                break;
-            case 3:
-                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 3>), grid, dim3(256), 0, st, Az, Bz, Cz,
-                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
-                break;
-            case 4:
-                hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 4>), grid, dim3(256), 0, st, Az, Bz, Cz,
-                                   Iz, p.M, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
-                break;
-            default:
-                return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
-        }
-        TG_HIP(hipGetLastError());
+    switch (kt) {
+        case 2:
+            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 2>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
+                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
+            break;
+        case 3:
+            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 3>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
+                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
+            break;
+        case 4:
+            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 4>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
+                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
+            break;
+        default:
+            return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
     }
+    TG_HIP(hipGetLastError());
     return TG_OK;
 }
 
