@@ -39,7 +39,7 @@ def _guards_ok(buf: torch.Tensor, nbytes: int) -> bool:
 
 
 def _shape(rng):
-    kind = rng.integers(0, 6)
+    kind = rng.integers(0, 7)
     if kind == 0:  # ragged, generic tiles
         return [int(x) for x in rng.integers(1, 300, size=3)], "ragged"
     if kind == 1:  # full tiles, direct-to-LDS
@@ -51,6 +51,9 @@ def _shape(rng):
     if kind == 3:  # split K: few tiles, long K
         return [64 * int(rng.integers(1, 3)), 512 * int(rng.integers(1, 9)),
                 64 * int(rng.integers(1, 3))], "split"
+    if kind == 5:  # short K, N % 64 == 0, any M
+        return [int(rng.integers(1, 700)), int(rng.choice([32, 64, 96, 128])),
+                64 * int(rng.integers(1, 6))], "short-k"
     if kind == 4:  # tiny and degenerate
         return [int(rng.integers(1, 5)), int(rng.integers(0, 40)), int(rng.integers(1, 5))], "tiny"
     return [64 * int(rng.integers(1, 4)), 32 * int(rng.integers(1, 8)),
@@ -77,6 +80,10 @@ def _data(rng, dt, shape, mode, inf):
         return rng.integers(-(1 << 20), 1 << 20, size=shape).astype(NP[dt])  # i32-key range
     if mode == 2:
         return rng.integers(0, 3, size=shape).astype(NP[dt])  # ties
+    if mode == 4:  # f32-key range with sparse outliers: some row tiles leave the key paths
+        x = rng.integers(-1000, 1001, size=shape)
+        x[rng.random(shape) < 0.002] = 1 << 16
+        return x.astype(NP[dt])
     info = np.iinfo(NP[dt])
     return rng.integers(info.max - 100, info.max, size=shape).astype(NP[dt])  # wraparound
 
@@ -95,14 +102,16 @@ def test_forward_fuzz(seed):
         (m, k, n), kind = _shape(rng)
         batch = int(rng.choice([1, 1, 2, 3]))
         with_argmax = bool(rng.random() < 0.8)
-        api = str(rng.choice(["ws", "alloc"]))
+        # "min": the documented minimum workspace (argmax: k x max(m, n)
+        # elements per product), which leaves out the split-K partials.
+        api = str(rng.choice(["ws", "alloc", "min"]))
         es = np.dtype(NP[dt]).itemsize
         # Strided batches: a gap of `gap` elements after every output matrix.
         gap = int(rng.choice([0, 0, 4, 12]))
         sc = m * n + gap
         print(f"[case] seed={seed} case={case} {kind} {sr} {dt} {layout} batch={batch} "
               f"m={m} k={k} n={n} argmax={with_argmax} api={api} gap={gap}", flush=True)
-        mode = int(rng.integers(0, 4 if dt in ("i32", "i64") else 3))
+        mode = int(rng.integers(0, 5 if dt in ("i32", "i64") else 3))
         inf = None if sr == "maxmul" else (np.inf if rng.random() < 0.5 else -np.inf)
         a = [_data(rng, dt, (m, k), mode, inf) for _ in range(batch)]
         b = [_data(rng, dt, (k, n), mode, inf) for _ in range(batch)]
@@ -119,19 +128,21 @@ def test_forward_fuzz(seed):
         cbuf = _guarded(c_bytes)
         ibuf = _guarded(i_bytes) if with_argmax else None
         ws_bytes = lib.tg_gemm_workspace_size(nat.DTYPE[dt], batch, m, n, k, int(with_argmax))
+        if api == "min":
+            ws_bytes = -(-(batch * k * max(m, n) * es) // 256) * 256 if with_argmax else 0
         wbuf = _guarded(ws_bytes + 256)  # room to align the workspace to 256 bytes
         woff = GUARD + (-(wbuf.data_ptr() + GUARD)) % 256
         sr_c, dt_c, lay_c = nat.SEMIRING[sr], nat.DTYPE[dt], nat.LAYOUT[layout]
         if batch == 1 and gap == 0 and rng.random() < 0.5:
             # The single-product entry points.
-            if api == "ws":
+            if api != "alloc":
                 rc = lib.tg_gemm_ws(0, sr_c, dt_c, lay_c, _p(ta), _p(tb), _p(cbuf, GUARD),
                                     _p(ibuf, GUARD) if with_argmax else None, m, n, k,
                                     _p(wbuf, woff), ws_bytes, stream)
             else:
                 rc = lib.tg_gemm(0, sr_c, dt_c, lay_c, _p(ta), _p(tb), _p(cbuf, GUARD),
                                  _p(ibuf, GUARD) if with_argmax else None, m, n, k, stream)
-        elif api == "ws":
+        elif api != "alloc":
             rc = lib.tg_gemm_strided_batched_ws(
                 0, sr_c, dt_c, lay_c, _p(ta), _p(tb), _p(cbuf, GUARD),
                 _p(ibuf, GUARD) if with_argmax else None, batch, m, n, k, m * k, k * n, sc,

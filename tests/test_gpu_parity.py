@@ -32,10 +32,21 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def min_workspace(a, k, m, n, with_argmax):
+    """The documented minimum workspace: k x max(m, n) elements per product
+    for argmax calls (B^T staging), rounded up to 256 bytes."""
+    if not with_argmax:
+        return 0
+    return -(-(k * max(m, n) * a.dtype.itemsize) // 256) * 256
+
+
 def gpu_gemm(sr, a, b, with_argmax=True, layout="row", api="alloc"):
-    """Run tg_gemm (api='alloc') or tg_gemm_ws (api='ws') through ctypes.
-    For layout='col' the numpy inputs are row-major logical matrices that are
-    handed over in column-major storage; results come back row-major."""
+    """Run tg_gemm (api='alloc') or tg_gemm_ws through ctypes, with
+    tg_gemm_workspace_size bytes (api='ws') or the documented minimum
+    (api='min', which runs products that need more than the minimum on the
+    kernels that do not).  For layout='col' the numpy inputs are row-major
+    logical matrices that are handed over in column-major storage; results
+    come back row-major."""
     nat = _nat()
     lib = nat.load()
     m, k = a.shape
@@ -53,7 +64,10 @@ def gpu_gemm(sr, a, b, with_argmax=True, layout="row", api="alloc"):
         nat.check(lib.tg_gemm(0, nat.SEMIRING[sr], dt, lay, _p(ta), _p(tb), _p(c), _p(am), m, n, k,
                               stream))
     else:
-        ws_bytes = lib.tg_gemm_workspace_size(dt, 1, m, n, k, int(with_argmax))
+        if api == "min":
+            ws_bytes = min_workspace(a, k, m, n, with_argmax)
+        else:
+            ws_bytes = lib.tg_gemm_workspace_size(dt, 1, m, n, k, int(with_argmax))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
         nat.check(lib.tg_gemm_ws(0, nat.SEMIRING[sr], dt, lay, _p(ta), _p(tb), _p(c), _p(am), m,
                                  n, k, _p(ws), ws_bytes, stream))
@@ -542,11 +556,14 @@ def test_workspace_bound_and_guard(layout, shape):
 
 # The K-resident kernel's three i32 paths, chosen per workgroup from the
 # magnitudes in its panels: f32 keys (all |x| < 2^15), i32 keys (< 2^22) and
-# the chunked path (anything larger, including wraparound).
+# the chunked path (anything larger, including wraparound).  The calls pass
+# the documented minimum workspace (k x max(m, n)), which the K-resident
+# kernel does not need at all.
 @pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
 def test_k_resident_integer_paths(sr):
     rng = np.random.default_rng(53)
     m, k, n = 256, 128, 128
+    api = "min"
     cases = {
         "f32-key boundary": (rng.choice([-32768, -32767, 0, 32766, 32767], size=(m, k)),
                              rng.choice([-32768, 32767, 1, -1], size=(k, n))),
@@ -561,15 +578,103 @@ def test_k_resident_integer_paths(sr):
         print(f"[case] k-resident {sr} i32 {name}", flush=True)
         a = a.astype(np.int32)
         b = b.astype(np.int32)
-        assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+        assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
     # One workgroup's panel (rows 64..127) holds a large value: that workgroup
     # takes the chunked path, the others keep the key paths.
     a = rng.integers(-1000, 1001, size=(m, k)).astype(np.int32)
     b = rng.integers(-50, 1, size=(k, n)).astype(np.int32)
     a[100, 7] = 1 << 24
-    assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+    assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
     a[100, 7] = 1 << 17
-    assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+    assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
+
+
+# Short-K i32 argmax over ragged and full-tile shapes (K in {32, 64, 96,
+# 128}, N a multiple of 64, M anything): the key-range boundary, ties,
+# wraparound, one row or one B entry just outside the f32-key range, and rows
+# that never beat the tropical zero.
+SHORT_K_SHAPES = [(1, 32, 64), (63, 64, 128), (200, 96, 192), (4113, 128, 128), (130, 128, 256),
+                  (77, 64, 320), (256, 128, 128)]
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus"])
+def test_short_k_integer_argmax(sr):
+    rng = np.random.default_rng(54 + (sr == "minplus"))
+    for (m, k, n) in SHORT_K_SHAPES:
+        cases = {
+            "viterbi": (rng.integers(-1000, 1001, size=(m, k)), rng.integers(-50, 1, size=(k, n))),
+            "key boundary": (rng.choice([-32768, -32767, 0, 32766, 32767], size=(m, k)),
+                             rng.choice([-32768, 32767, 1, -1], size=(k, n))),
+            "ties": (rng.integers(0, 3, size=(m, k)), rng.integers(0, 3, size=(k, n))),
+            "wraparound": (rng.integers(2**31 - 60, 2**31 - 1, size=(m, k)),
+                           rng.integers(-5, 60, size=(k, n))),
+        }
+        # One row just outside the f32-key range.
+        a = rng.integers(-1000, 1001, size=(m, k))
+        a[m // 2, k - 1] = 32768
+        cases["one wave chunked"] = (a, rng.integers(-50, 1, size=(k, n)))
+        # One B entry just outside it.
+        b = rng.integers(-50, 1, size=(k, n))
+        b[k // 3, n - 1] = -32769
+        cases["one block chunked"] = (rng.integers(-1000, 1001, size=(m, k)), b)
+        # Rows that never beat the tropical zero keep it, with argmax 0.
+        a = rng.integers(-1000, 1001, size=(m, k))
+        zero = -(2**31) if sr == "maxplus" else 2**31 - 1
+        a[0, :] = zero
+        cases["zero row"] = (a, np.zeros((k, n), np.int64))
+        for name, (a, b) in cases.items():
+            print(f"[case] short-k {sr} m={m} k={k} n={n} {name}", flush=True)
+            a = a.astype(np.int32)
+            b = b.astype(np.int32)
+            ref = oracle.gemm(sr, a, b)
+            for api in ("alloc", "ws", "min"):
+                assert_exact(*gpu_gemm(sr, a, b, True, api=api), *ref)
+
+
+def test_short_k_integer_layouts_batches_and_guard():
+    """Column-major calls (the kernels' N is m), strided batches with gaps in
+    which one item leaves the f32-key range, and a guard after exactly
+    tg_gemm_workspace_size bytes of workspace."""
+    nat = _nat()
+    lib = nat.load()
+    rng = np.random.default_rng(56)
+    a = rng.integers(-1000, 1001, size=(128, 64)).astype(np.int32)
+    b = rng.integers(-1000, 1001, size=(64, 1000)).astype(np.int32)
+    c, am = gpu_gemm("maxplus", a, b, True, layout="col")
+    assert_exact(c, am, *oracle.gemm("maxplus", a, b))
+
+    batch, m, k, n = 3, 300, 96, 192
+    gap_a, gap_c = 40, 24
+    items = [(rng.integers(-1000, 1001, size=(m, k)), rng.integers(-50, 1, size=(k, n)))
+             for _ in range(batch)]
+    items[1][0][5, 5] = 1 << 20  # this item's first row tile leaves the f32-key range
+    sa, sb, sc = m * k + gap_a, k * n, m * n + gap_c
+    ha = np.zeros(batch * sa, np.int32)
+    hb = np.zeros(batch * sb, np.int32)
+    for t, (x, y) in enumerate(items):
+        ha[t * sa:t * sa + m * k] = x.ravel()
+        hb[t * sb:t * sb + k * n] = y.ravel()
+    for sr in ("maxplus", "minplus"):
+        ws_bytes = lib.tg_gemm_workspace_size(nat.DTYPE["i32"], batch, m, n, k, 1)
+        guard = 65536
+        ws = torch.full((ws_bytes + guard,), 0xA5, dtype=torch.uint8, device=DEV)
+        c3 = torch.full((batch * sc,), 7, dtype=torch.int32, device=DEV)
+        am3 = torch.full((batch * sc,), 7, dtype=torch.int32, device=DEV)
+        ta, tb = _dev(ha), _dev(hb)
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        nat.check(lib.tg_gemm_strided_batched_ws(0, nat.SEMIRING[sr], nat.DTYPE["i32"],
+                                                 nat.LAYOUT["row"], _p(ta), _p(tb), _p(c3),
+                                                 _p(am3), batch, m, n, k, sa, sb, sc, _p(ws),
+                                                 ws_bytes, stream))
+        torch.cuda.synchronize()
+        assert bool(torch.all(ws[ws_bytes:] == 0xA5)), "workspace overrun"
+        cv, iv = c3.cpu().numpy(), am3.cpu().numpy()
+        for t, (x, y) in enumerate(items):
+            assert_exact(cv[t * sc:t * sc + m * n].reshape(m, n),
+                         iv[t * sc:t * sc + m * n].reshape(m, n),
+                         *oracle.gemm(sr, x.astype(np.int32), y.astype(np.int32)))
+            assert np.all(cv[t * sc + m * n:(t + 1) * sc] == 7), "gap after C overwritten"
+            assert np.all(iv[t * sc + m * n:(t + 1) * sc] == 7), "gap after argmax overwritten"
 
 
 # Split K: full-tile 32-bit problems with few 64 x 64 tiles run K in slices

@@ -282,9 +282,38 @@ int current_cu_count() {
     return cache[dev];
 }
 
-// K-resident argmax kernel for short K (32-bit types): no B^T staging.  A
-// persistent grid of two workgroups per CU (their LDS panels allow two),
-// each owning one column tile.
+// Workgroups of tg_gemm_kres<SR, T, KT> resident per CU (LDS and register
+// limits), from the runtime's occupancy calculator; 2 if that fails.
+template <int SR, typename T, int KT>
+int kres_per_cu() {
+    static const int n = [] {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, tg::tg_gemm_kres<SR, T, KT>, 256, 0) !=
+                hipSuccess ||
+            b <= 0) {
+            (void)hipGetLastError();
+            b = 2;
+        }
+        return b;
+    }();
+    return n;
+}
+
+template <int SR, typename T, int KT>
+void launch_kres(const Problem& p, int64_t tiles_m, int64_t tiles_n, hipStream_t st) {
+    // Persistent grid: every resident workgroup slot, rounded down to a
+    // multiple of the column-tile count (each workgroup owns one column tile).
+    const int64_t total = p.batch * tiles_m * tiles_n;
+    int64_t grid = int64_t(kres_per_cu<SR, T, KT>()) * current_cu_count();
+    grid = (grid / tiles_n) * tiles_n;
+    if (grid < tiles_n) grid = tiles_n;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, KT>), dim3(unsigned(grid)), dim3(256), 0, st,
+                       static_cast<const T*>(p.A), static_cast<const T*>(p.B), static_cast<T*>(p.C),
+                       p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
+}
+
+// K-resident argmax kernel for short K (32-bit types): no B^T staging.
 template <int SR, typename T>
 int run_gemm_kres(const Problem& p, hipStream_t st) {
     using Cfg = tg::KresCfg;
@@ -292,32 +321,12 @@ int run_gemm_kres(const Problem& p, hipStream_t st) {
     const int64_t tiles_n = p.N / Cfg::BN;
     if (tiles_m > 0x7fffffffLL || tiles_n > 0x7fffffffLL)
         return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
-    const int64_t total = p.batch * tiles_m * tiles_n;
-    int64_t grid = int64_t(2) * current_cu_count();
-    grid = (grid / tiles_n) * tiles_n;
-    if (grid < tiles_n) grid = tiles_n;
-    if (grid > total) grid = total;
-    if (grid > 0x7fffffffLL) return fail(TG_ERR_DIMENSION_MISMATCH, "too many column tiles");
-    const T* A = static_cast<const T*>(p.A);
-    const T* B = static_cast<const T*>(p.B);
-    T* C = static_cast<T*>(p.C);
     KernelTimer timer(st);
-    const int kt = int(p.K / Cfg::BK);
-    switch (kt) {
-        case 2:
-            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 2>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
-                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
-            break;
-        case 3:
-            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 3>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
-                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
-            break;
-        case 4:
-            hipLaunchKernelGGL((tg::tg_gemm_kres<SR, T, 4>), dim3(unsigned(grid)), dim3(256), 0, st, A, B,
-                               C, p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
-            break;
-        default:
-            return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
+    switch (p.K / Cfg::BK) {
+        case 2: launch_kres<SR, T, 2>(p, tiles_m, tiles_n, st); break;
+        case 3: launch_kres<SR, T, 3>(p, tiles_m, tiles_n, st); break;
+        case 4: launch_kres<SR, T, 4>(p, tiles_m, tiles_n, st); break;
+        default: return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
     }
     TG_HIP(hipGetLastError());
     return TG_OK;
