@@ -6,9 +6,10 @@
 // stays in LDS, so the argmax is resolved from LDS: no B^T staging kernel, no
 // global re-reads and no chunk sort.
 //
-// Persistent: the grid holds two workgroups per CU.  Workgroup w owns column
-// tile w % tiles_n and walks the row tiles (over all batch items) with a
-// stride of gridDim.x / tiles_n.  Its B panel (K x 64) stays in LDS across
+// Persistent: the grid holds every resident workgroup slot (two per CU for
+// K = 128).  Workgroup w (renumbered per XCD) owns column tile w % tiles_n
+// and walks the row tiles (over all batch items) with a stride of
+// gridDim.x / tiles_n.  Its B panel (K x 64) stays in LDS across
 // row tiles and is reloaded only when the batch item or the path changes; the
 // next row tile's A panel (64 x K) is prefetched into registers while the
 // current one computes, then range-checked and written to LDS.
@@ -88,11 +89,18 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     const int tx = tid & 15;
     const int ty = tid >> 4;
     const int swz = ty & 7;
-    const int tn = int(blockIdx.x) % tiles_n;
+    // Consecutive workgroup ids go round-robin over the 8 XCDs.  Renumber so
+    // each XCD holds a contiguous range: the workgroups that share a row tile
+    // (one per column tile) then sit on one XCD and read its A panel through
+    // the same L2, so A is fetched from HBM once.
+    int lb = int(blockIdx.x);
+    if ((gridDim.x & 7) == 0 && (int(gridDim.x >> 3) % tiles_n) == 0)
+        lb = int(blockIdx.x & 7) * int(gridDim.x >> 3) + int(blockIdx.x >> 3);
+    const int tn = lb % tiles_n;
     const int64_t step = int64_t(gridDim.x) / tiles_n;
     const int64_t total = batch * tiles_m;
     const int64_t col0 = int64_t(tn) * BN;
-    int64_t r = int64_t(blockIdx.x) / tiles_n;
+    int64_t r = int64_t(lb) / tiles_n;
     if (r >= total) return;
 
     // ---- staging helpers ----------------------------------------------------
