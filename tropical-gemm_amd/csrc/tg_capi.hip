@@ -353,18 +353,21 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
         if (splits > 1 && ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, splits).total > ws_bytes)
             splits = 1;
         const int64_t ks = p.K / splits;
-        // Argmax chunk length: bookkeeping costs ~2 ops per output per chunk
-        // (2K/CL) and the exact resolve ~4 ops per product of one chunk
-        // (4*CL per slice); the sum is smallest near CL = sqrt(K/2) per slice.
-        const int cl = !argmax ? 32 : ks <= 192 ? 8 : ks <= 768 ? 16 : 32;
+        // Argmax chunk length.  The bookkeeping costs 2 VALU ops per output per
+        // chunk (2K/CL); the resolve re-reads one chunk's A-row and B^T-row
+        // segments per output from L2 and recomputes them, which costs more
+        // than its ~4 ops per product suggest.  Measured on MI355X (f32
+        // MaxPlus, slices of 256 .. 4096 k): CL = 8 is fastest up to 512 k
+        // per slice, CL = 16 above (CL = 32 is 4-18% slower everywhere).
+        const int cl = !argmax ? 32 : ks <= 512 ? 8 : 16;
         // 64 x 128 tiles for argmax problems big enough that the last round
         // of 768 resident workgroups is a small share of the work (their
         // main loop is the faster one); 64 x 64 tiles otherwise (value-only
         // runs four workgroups per CU, small problems get twice the tiles).
-        const bool wide = splits == 1 && argmax && cl == 32 && p.N % tg::DlCfg<8>::BN == 0 &&
+        const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
                           (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
-        if (wide && tg::dl_fits<8, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 8, 32>(p, ws, 1, st);
+        if (wide && tg::dl_fits<8, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+            return run_gemm_dl<SR, T, 8, 16>(p, ws, 1, st);
         if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
             return run_gemm_dl<SR, T, 4, 8>(p, ws, splits, st);
         if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
