@@ -98,6 +98,110 @@ def run_cpu_baseline(rows: int) -> dict:
     }
 
 
+def run_einsum(args, lib, dev) -> int:
+    """Einsum workload: a step is one ``tropical_gemm.einsum`` call on operands
+    resident in HBM (contraction order, permutation copies and the GEMMs).
+    The roofline is for the GEMM kernels, timed by the library's hook; their
+    share of the step shows what the permutations and host planning cost."""
+    import torch
+
+    import workloads
+    from tropical_gemm import _native as nat
+    from tropical_gemm import einsum as E
+
+    cfg = workloads.EINSUM[args.config]
+    ops_ = workloads.make_einsum_operands(args.config, dev)
+    code, sr = cfg["code"], cfg["semiring"]
+    ixs, iy = E.parse(code)
+    sizes = cfg["sizes"]
+    path = E.einsum_path(ixs, iy, sizes, "greedy")
+    # Tropical ops of the contraction tree: 2 per term of every pairwise GEMM.
+    labs = [list(x) for x in ixs]
+    ops = 0.0
+    gemms = []
+    for i, j in path:
+        keep = set(iy)
+        for o, lab in enumerate(labs):
+            if o not in (i, j):
+                keep.update(lab)
+        union = list(dict.fromkeys(labs[i] + labs[j]))
+        res = [x for x in union if x in keep]
+        terms = 1
+        for x in union:
+            terms *= sizes[x]
+        ops += 2.0 * terms
+        gemms.append("".join(labs[i]) + "," + "".join(labs[j]) + "->" + "".join(res))
+        labs = [lab for o, lab in enumerate(labs) if o not in (i, j)] + [res]
+
+    def step():
+        return E.einsum(code, *ops_, semiring=sr)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    tot = ctypes.c_double(0.0)
+    nl = ctypes.c_int64(0)
+    nat.check(lib.tg_kernel_timing_read(ctypes.byref(tot), ctypes.byref(nl)))  # clear
+    nat.check(lib.tg_kernel_timing_enable(1))
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize(dev)
+    nat.check(lib.tg_kernel_timing_enable(0))
+    nat.check(lib.tg_kernel_timing_read(ctypes.byref(tot), ctypes.byref(nl)))
+    ms_gemms = tot.value / args.steps  # every GEMM kernel of one step
+    gops = ops / (ms_step / 1e3) / 1e9
+    kernel_tops = ops / (ms_gemms / 1e3) / 1e12
+    out = {
+        "metric": METRIC,
+        "value": round(gops, 2),
+        "unit": "GOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded torch Philox on device; workloads.py)",
+        "config": {"workload": f"{args.config}: tropical einsum {code} ({sr}, value-only)",
+                   "sizes": sizes, "contraction_path": gemms,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {
+            "bound": "valu",
+            "achieved": round(kernel_tops, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4),
+            "traffic": None,
+            "kernel": "tg_gemm_dl<MaxPlus, f32, value-only> (every GEMM of the contraction)",
+            "kernel_ms": round(ms_gemms, 4),
+            "kernel_launches_timed": int(nl.value),
+            "ops_per_launch": ops / max(len(gemms), 1),
+            "trop_peak": TROP_PEAK_TOPS,
+            "frac_of_trop_peak": round(kernel_tops / TROP_PEAK_TOPS, 4),
+        },
+        "gemm_share_of_step": round(ms_gemms / ms_step, 4),
+        "step_frac_of_trop_peak": round(gops / 1e3 / TROP_PEAK_TOPS, 4),
+        "wall_s_timed_region": round(wall, 4),
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,7 +209,7 @@ def main() -> int:
     # The engine clock ramps from ~2.1 to ~2.35 GHz over the first ~15 ms of
     # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
     ap.add_argument("--warmup", type=int, default=25)
-    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4", "C5", "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -128,6 +232,8 @@ def main() -> int:
         return 1
     lib = nat.load()
     dev = torch.device("cuda", 0)
+    if args.config in workloads.EINSUM:
+        return run_einsum(args, lib, dev)
     cfg = workloads.CONFIGS[args.config]
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
     a, b = workloads.make_inputs(args.config, dev)

@@ -10,6 +10,8 @@ the host) to the CPU oracle.  Nothing here reads the reference.
     C3  MaxMul f32 value-only, M=8192 K=2048 N=4096, entries in (0,1]
     C4  MaxPlus i32 M=262144 K=128 N=128 with argmax; A in [-1000,1000], B in [-50,0]
     C5  P forward, then backward with dC ~ N(0,1)
+    E1  tropical einsum "jik,lkj,lm->im", MaxPlus f32, N(0,1): i = l = m = 2048,
+        j = 32, k = 64 (two 2048^3 contractions after two permutations)
 """
 from __future__ import annotations
 
@@ -71,6 +73,21 @@ def _distance_matrix(r, c, device, g_val, g_mask):
     idx = torch.arange(diag, device=device)
     d[idx, idx] = 0.0
     return d
+
+
+EINSUM = {
+    "E1": dict(code="jik,lkj,lm->im", semiring="maxplus", dtype="f32",
+               sizes=dict(i=2048, j=32, k=64, l=2048, m=2048)),
+}
+
+
+def make_einsum_operands(name: str, device="cuda"):
+    """Operands of einsum workload `name` (seeded like the GEMM configs)."""
+    cfg = EINSUM[name]
+    idx = len(CONFIGS) + list(EINSUM).index(name)
+    lhs = cfg["code"].split("->")[0].split(",")
+    return [torch.randn([cfg["sizes"][x] for x in term], generator=_gen(device, idx, t),
+                        device=device) for t, term in enumerate(lhs)]
 
 
 def make_grad(name: str, m: int, n: int, device="cuda", dtype=torch.float32):
