@@ -25,7 +25,10 @@ summed inside one operand are reduced first, as a product with a column of
 the semiring's one (0 for MaxPlus/MinPlus, 1 for MaxMul).
 
 Permutations and reshapes are torch views and copies (data movement only, the
-plan's cuTENSOR step); every (+)/(x) runs in the HIP kernels.  Gradients flow
+plan's cuTENSOR step); every (+)/(x) runs in the HIP kernels.  Inside an
+einsum, which operand is the GEMM's left one and the order of the contracted
+labels are chosen so that the fewest elements are copied (an operand whose
+permuted view is already contiguous costs nothing).  Gradients flow
 through the library's autograd functions (float32/float64), so an einsum of
 tensors that require grad is differentiable.
 """
@@ -134,6 +137,19 @@ def contract_binary(a, b, ia: Sequence, ib: Sequence, iy: Sequence, semiring: st
     nothing is contracted).  Labels that appear in one operand only and not in
     the output are summed inside that operand first; their argmax is not
     tracked, so ``with_argmax`` requires that there are none."""
+    return _contract(a, b, ia, ib, iy, semiring, with_argmax, False)
+
+
+def _copy_cost(t: torch.Tensor, perm: list) -> int:
+    """Elements copied to lay ``t`` out in the order ``perm`` (0 when the
+    permuted view is already contiguous)."""
+    return 0 if t.permute(perm).is_contiguous() else t.numel()
+
+
+def _contract(a, b, ia, ib, iy, semiring, with_argmax, fewest_copies):
+    """contract_binary; with ``fewest_copies`` the operand order and the order
+    of the contracted labels (both free when no argmax is returned) are chosen
+    to copy the fewest elements into GEMM layout."""
     _check_semiring(semiring)
     a = ops.as_tensor(a)
     b = ops.as_tensor(b)
@@ -158,6 +174,21 @@ def contract_binary(a, b, ia: Sequence, ib: Sequence, iy: Sequence, semiring: st
     size.update({x: b.shape[ib.index(x)] for x in ib})
 
     batch, left, right, con = cls["batch"], cls["left"], cls["right"], cls["contracted"]
+    if fewest_copies:
+        # Candidates: (swap operands?, contracted-label order); the first one
+        # is the documented layout, kept on ties.
+        cands = []
+        for swap in (False, True):
+            x, lx, y, ly = (b, ib, a, ia) if swap else (a, ia, b, ib)
+            lft, rgt = (right, left) if swap else (left, right)
+            for order in (con, [c for c in ly if c in con]):
+                cost = (_copy_cost(x, [lx.index(c) for c in batch + lft + order]) +
+                        _copy_cost(y, [ly.index(c) for c in batch + order + rgt]))
+                cands.append((cost, len(cands), swap, order))
+        _, _, swap, con = min(cands)
+        if swap:
+            a, ia, b, ib = b, ib, a, ia
+            left, right = right, left
     nb = _prod(size[x] for x in batch)
     m = _prod(size[x] for x in left)
     n = _prod(size[x] for x in right)
@@ -329,7 +360,7 @@ def einsum(code: str, *operands, semiring: str = "maxplus", optimize="greedy") -
                 keep.update(lab)
         (ta, la), (tb, lb) = cur[i], cur[j]
         res = _pair_result(la, lb, keep)
-        tc = contract_binary(ta, tb, la, lb, res, semiring)
+        tc = _contract(ta, tb, la, lb, res, semiring, False, True)
         cur = [c for o, c in enumerate(cur) if o not in (i, j)] + [(tc, res)]
 
     t, lab = cur[0]
