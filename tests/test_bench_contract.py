@@ -1,0 +1,51 @@
+"""bench.py keeps the driver's contract: one JSON line with the metric, the
+step timing, the roofline and (config P) the CPU baseline; more than one GPU
+is refused with a message."""
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KEYS = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+        "scaling", "vs_baseline", "dtype", "data", "config", "roofline"]
+ROOFLINE = ["bound", "achieved", "peak", "unit", "frac", "traffic"]
+
+
+def _bench(*args, timeout=240):
+    return subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], cwd=ROOT,
+                          capture_output=True, text=True, timeout=timeout)
+
+
+def test_more_than_one_gpu_is_refused():
+    r = _bench("--gpus", "2", timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("args", [("--config", "P", "--cpu-rows", "64"),
+                                  ("--config", "C1", "--cpu-rows", "0"),
+                                  ("--config", "E1")], ids=["P", "C1", "E1"])
+def test_json_line(args):
+    print(f"[case] bench.py {' '.join(args)}", flush=True)
+    r = _bench(*args, "--steps", "2", "--warmup", "1")
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1, r.stdout
+    out = json.loads(lines[0])
+    for key in KEYS:
+        assert key in out, key
+    assert out["n_gpus"] == 1 and out["steps"] == 2 and out["warmup"] == 1
+    assert out["higher_is_better"] is True and out["value"] > 0 and out["ms_per_step"] > 0
+    assert "workload" in out["config"]
+    for key in ROOFLINE:
+        assert key in out["roofline"], key
+    roof = out["roofline"]
+    assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    if args[1] == "P":
+        base = out["cpu_baseline"]
+        assert base["value"] > 0 and base["cores"] == 1 and base["kind"] in ("port", "reference")
+        assert out["argmax_consistency_check"] is True
