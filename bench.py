@@ -53,14 +53,14 @@ KERNEL_NAMES = {
     "C1": "tg_gemm_dl<MaxPlus, f32, argmax> split-K x4 + tg_merge_splits",
     "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
-    "C4": "tg_gemm_kres<MaxPlus, i32, K=128> (f32 keys)",
+    "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md).
 # Configs not profiled: None.
-TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9}
+TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.439e9}
 
 
 def cpu_model() -> str:

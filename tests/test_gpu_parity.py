@@ -589,6 +589,69 @@ def test_k_resident_integer_paths(sr):
     assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
 
 
+def _strided_batched(sr, items, gap_a=24, gap_c=40):
+    """Run tg_gemm_strided_batched_ws on a list of (A, B) with gaps after
+    every A and C; return the per-item (C, argmax) and check the gaps."""
+    nat = _nat()
+    lib = nat.load()
+    m, k = items[0][0].shape
+    n = items[0][1].shape[1]
+    batch = len(items)
+    dt = DT_NAME[items[0][0].dtype]
+    sa, sb, sc = m * k + gap_a, k * n, m * n + gap_c
+    ha = np.zeros(batch * sa, items[0][0].dtype)
+    hb = np.zeros(batch * sb, items[0][0].dtype)
+    for t, (x, y) in enumerate(items):
+        ha[t * sa:t * sa + m * k] = x.ravel()
+        hb[t * sb:t * sb + k * n] = y.ravel()
+    ta, tb = _dev(ha), _dev(hb)
+    c3 = torch.full((batch * sc,), 7, dtype=TORCH_DT[items[0][0].dtype], device=DEV)
+    am3 = torch.full((batch * sc,), 7, dtype=torch.int32, device=DEV)
+    ws_bytes = lib.tg_gemm_workspace_size(nat.DTYPE[dt], batch, m, n, k, 1)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.check(lib.tg_gemm_strided_batched_ws(0, nat.SEMIRING[sr], nat.DTYPE[dt], nat.LAYOUT["row"],
+                                             _p(ta), _p(tb), _p(c3), _p(am3), batch, m, n, k, sa,
+                                             sb, sc, _p(ws), ws_bytes, stream))
+    torch.cuda.synchronize()
+    cv, iv = c3.cpu().numpy(), am3.cpu().numpy()
+    out = []
+    for t in range(batch):
+        assert np.all(cv[t * sc + m * n:(t + 1) * sc] == 7), "gap after C overwritten"
+        assert np.all(iv[t * sc + m * n:(t + 1) * sc] == 7), "gap after argmax overwritten"
+        out.append((cv[t * sc:t * sc + m * n].reshape(m, n), iv[t * sc:t * sc + m * n].reshape(m, n)))
+    return out
+
+
+# The K-resident kernel with 64 x 128 tiles (i32 MaxPlus/MinPlus, N a
+# multiple of 128): batch items change the resident B panel; a row tile that
+# leaves the f32-key range turns the B panel raw for the chunked path and the
+# next tile turns it back into keys; a batch item whose B panel is out of
+# range runs every tile chunked.
+@pytest.mark.parametrize("sr", ["maxplus", "minplus"])
+def test_k_resident_wide_tiles(sr):
+    rng = np.random.default_rng(57 + (sr == "minplus"))
+    for (m, k, n, batch) in [(256, 64, 256, 1), (512, 96, 128, 3), (384, 128, 384, 2),
+                             (4096, 128, 128, 2)]:
+        print(f"[case] k-resident 64x128 {sr} m={m} k={k} n={n} batch={batch}", flush=True)
+        items = []
+        for t in range(batch):
+            a = rng.integers(-1000, 1001, size=(m, k))
+            b = rng.integers(-50, 1, size=(k, n))
+            a[70 + t, 3] = 40000  # row tile 1 leaves the key range
+            if t == 1:
+                b[3, 5] = 1 << 20  # this item's whole B panel does
+            items.append((a.astype(np.int32), b.astype(np.int32)))
+        for (c, am), (a, b) in zip(_strided_batched(sr, items), items):
+            assert_exact(c, am, *oracle.gemm(sr, a, b))
+        for name, lo, hi in (("ties", 0, 3), ("wraparound", 2**31 - 60, 2**31 - 1)):
+            a = rng.integers(lo, hi, size=(m, k)).astype(np.int32)
+            b = rng.integers(0 if name == "ties" else -5, 3 if name == "ties" else 60,
+                             size=(k, n)).astype(np.int32)
+            for api in ("alloc", "min"):
+                assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
+
+
 # Short-K i32 argmax over ragged and full-tile shapes (K in {32, 64, 96,
 # 128}, N a multiple of 64, M anything): the key-range boundary, ties,
 # wraparound, one row or one B entry just outside the f32-key range, and rows

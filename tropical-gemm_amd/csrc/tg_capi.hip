@@ -17,6 +17,7 @@
 #include "../../include/tropical_gemm_hip.h"
 #include "tg_gemm_dl.hpp"
 #include "tg_gemm_kres.hpp"
+#include "tg_gemm_kres8.hpp"
 #include "tg_kernels.hpp"
 
 namespace {
@@ -313,6 +314,54 @@ void launch_kres(const Problem& p, int64_t tiles_m, int64_t tiles_n, hipStream_t
                        p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n), p.batch);
 }
 
+// Workgroups of tg_gemm_kres8<SR, KT> resident per CU; 1 if the query fails.
+template <int SR, int KT>
+int kres8_per_cu() {
+    static const int n = [] {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, tg::tg_gemm_kres8<SR, KT>, 256, 0) !=
+                hipSuccess ||
+            b <= 0) {
+            (void)hipGetLastError();
+            b = 1;
+        }
+        return b;
+    }();
+    return n;
+}
+
+template <int SR, int KT>
+void launch_kres8(const Problem& p, int64_t tiles_m, int64_t tiles_n, hipStream_t st) {
+    const int64_t total = p.batch * tiles_m * tiles_n;
+    int64_t grid = int64_t(kres8_per_cu<SR, KT>()) * current_cu_count();
+    grid = (grid / tiles_n) * tiles_n;
+    if (grid < tiles_n) grid = tiles_n;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL((tg::tg_gemm_kres8<SR, KT>), dim3(unsigned(grid)), dim3(256), 0, st,
+                       static_cast<const int32_t*>(p.A), static_cast<const int32_t*>(p.B),
+                       static_cast<int32_t*>(p.C), p.IDX, p.N, p.sA, p.sB, p.sC, int(tiles_m),
+                       int(tiles_n), p.batch);
+}
+
+// K-resident argmax kernel with 64 x 128 tiles (i32 MaxPlus/MinPlus).
+template <int SR>
+int run_gemm_kres8(const Problem& p, hipStream_t st) {
+    using Cfg = tg::Kres8Cfg;
+    const int64_t tiles_m = p.M / Cfg::BM;
+    const int64_t tiles_n = p.N / Cfg::BN;
+    if (tiles_m > 0x7fffffffLL || tiles_n > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    KernelTimer timer(st);
+    switch (p.K / Cfg::BK) {
+        case 2: launch_kres8<SR, 2>(p, tiles_m, tiles_n, st); break;
+        case 3: launch_kres8<SR, 3>(p, tiles_m, tiles_n, st); break;
+        case 4: launch_kres8<SR, 4>(p, tiles_m, tiles_n, st); break;
+        default: return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
+    }
+    TG_HIP(hipGetLastError());
+    return TG_OK;
+}
+
 // K-resident argmax kernel for short K (32-bit types): no B^T staging.
 template <int SR, typename T>
 int run_gemm_kres(const Problem& p, hipStream_t st) {
@@ -342,6 +391,11 @@ bool uses_kres(tg_dtype dt, const Problem& p) {
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
     if constexpr (sizeof(T) == 4) {
+        if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL) {
+            if (p.IDX != nullptr &&
+                tg::kres8_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
+                return run_gemm_kres8<SR>(p, st);
+        }
         if (p.IDX != nullptr &&
             tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
             return run_gemm_kres<SR, T>(p, st);
