@@ -60,7 +60,7 @@ KERNEL_NAMES = {
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md).
 # Configs not profiled: None.
-TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.439e9}
+TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9}
 
 
 def cpu_model() -> str:

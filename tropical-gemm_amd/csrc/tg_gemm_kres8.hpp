@@ -54,7 +54,8 @@ inline bool kres8_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, 
                        const void* A, const void* B, const void* C, const void* IDX) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     using Cfg = Kres8Cfg;
-    return M > 0 && N > 0 && M % Cfg::BM == 0 && N % Cfg::BN == 0 && K % Cfg::BK == 0 &&
+    return M > 0 && N > 0 && N < (int64_t(1) << 30) && M % Cfg::BM == 0 && N % Cfg::BN == 0 &&
+           K % Cfg::BK == 0 &&
            K >= int64_t(Cfg::BK) * Cfg::KT_MIN && K <= int64_t(Cfg::BK) * Cfg::KT_MAX &&
            sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) && a16(IDX);
 }
@@ -142,10 +143,15 @@ tg_gemm_kres8(const int32_t* __restrict__ A, const int32_t* __restrict__ B,
     // two k rows (1 KB).  Ends with a barrier.
     auto load_b = [&](int64_t z) {
         const int32_t* bz = B + z * sB + col0;
+        // The lane's offset inside a row pair.  The empty asm keeps the
+        // compiler from precomputing all BPW addresses once and holding them
+        // (in spilled registers) across the whole kernel.
+        int32_t lane_off = (lane >> 5) * int32_t(N) + (lane & 31) * 4;
+        asm volatile("" : "+v"(lane_off));
 #pragma unroll
         for (int q = 0; q < BPW; ++q) {
             const int p = wave * BPW + q;  // k row pair
-            lds_load16(bz + int64_t(2 * p + (lane >> 5)) * N + (lane & 31) * 4, Bs + p * 2 * BN);
+            lds_load16(bz + int64_t(2 * p) * N + lane_off, Bs + p * 2 * BN);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
