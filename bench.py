@@ -39,6 +39,7 @@ PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector (and dense) peak
 # densest mix (v_add_f32 + half a v_max3_f32) issues 2 tropical ops per 4
 # wave64-cycles per lane, i.e. half the FMA peak: 78.6e12 ops/s at 2.4 GHz.
 TROP_PEAK_TOPS = PEAK_FP32_TFLOPS / 2
+PEAK_HBM_GBS = 8000.0         # MI355X published HBM3E bandwidth
 DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
 WORKLOAD_NAMES = {
     "P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
@@ -47,6 +48,7 @@ WORKLOAD_NAMES = {
     "C3": "C3: MaxMul f32 8192x2048x4096 value-only",
     "C4": "C4: MaxPlus i32 262144x128x128 +argmax",
     "C5": "C5: MaxPlus f32 4096^3 +argmax forward, then grad_A and grad_B backward",
+    "M1": "M1: MaxPlus f32 65536x2048x8 +argmax (short K, HBM-bound)",
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
@@ -55,12 +57,14 @@ KERNEL_NAMES = {
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
     "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
+    "M1": "tg_gemm_tiles<MaxPlus, f32, argmax, exact> (128x64 tiles, per-product index)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
-# (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md).
+# (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md,
+# profiles/tg_gemm_tiles_exact_*.md).
 # Configs not profiled: None.
-TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9}
+TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9, "M1": 1.082e9}
 
 
 def cpu_model() -> str:
@@ -209,7 +213,8 @@ def main() -> int:
     # The engine clock ramps from ~2.1 to ~2.35 GHz over the first ~15 ms of
     # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
     ap.add_argument("--warmup", type=int, default=25)
-    ap.add_argument("--config", default="P", choices=["P", "C1", "C2", "C3", "C4", "C5", "E1"])
+    ap.add_argument("--config", default="P",
+                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -324,6 +329,27 @@ def main() -> int:
     kernel_tops = ops / (ms_kernel / 1e3) / 1e12
     esize = a.element_size()
     algo_bytes = esize * (m * k + k * n + m * n) + (4 * m * n if am is not None else 0)
+    if cfg.get("bound") == "hbm":
+        # Short K: the output (and argmax) writes dominate; the roofline is
+        # HBM bandwidth, achieved = algorithmic bytes / kernel time.
+        kernel_gbs = algo_bytes / (ms_kernel / 1e3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(kernel_gbs, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(kernel_gbs / PEAK_HBM_GBS, 4)}
+    else:
+        # Tropical (+)/(x) has no MFMA form: the kernel is bound by the
+        # vector ALU.  peak = MI355X published FP32 vector/dense peak.
+        roofline = {"bound": "valu", "achieved": round(kernel_tops, 3), "peak": PEAK_FP32_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4)}
+    roofline.update({
+        "traffic": TRAFFIC.get(args.config),
+        "kernel": KERNEL_NAMES[args.config],
+        "kernel_ms": round(ms_kernel, 4),
+        "kernel_launches_timed": int(nl.value),
+        "ops_per_launch": ops,
+        "trop_peak": TROP_PEAK_TOPS,
+        "frac_of_trop_peak": round(kernel_tops / TROP_PEAK_TOPS, 4),
+        "algorithmic_bytes": algo_bytes,
+    })
     out = {
         "metric": METRIC,
         "value": round(gops, 2),
@@ -340,23 +366,7 @@ def main() -> int:
         "config": {"workload": WORKLOAD_NAMES[args.config],
                    "semiring": cfg["semiring"], "m": m, "n": n, "k": k,
                    "argmax": cfg["argmax"], "layout": "row-major", "parallelism": "none (1 GPU)"},
-        "roofline": {
-            # Tropical (+)/(x) has no MFMA form: the kernel is bound by the
-            # vector ALU.  peak = MI355X published FP32 vector/dense peak.
-            "bound": "valu",
-            "achieved": round(kernel_tops, 3),
-            "peak": PEAK_FP32_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4),
-            "traffic": TRAFFIC.get(args.config),
-            "kernel": KERNEL_NAMES[args.config],
-            "kernel_ms": round(ms_kernel, 4),
-            "kernel_launches_timed": int(nl.value),
-            "ops_per_launch": ops,
-            "trop_peak": TROP_PEAK_TOPS,
-            "frac_of_trop_peak": round(kernel_tops / TROP_PEAK_TOPS, 4),
-            "algorithmic_bytes": algo_bytes,
-        },
+        "roofline": roofline,
         "step_frac_of_trop_peak": round(gops / 1e3 / TROP_PEAK_TOPS, 4),
         "wall_s_timed_region": round(wall, 4),
         "argmax_consistency_check": check,

@@ -89,7 +89,7 @@ int tg_stream_synchronize(int device, void* stream);
 
 /* ---- kernel timing (diagnostics) ----------------------------------------
  * No counterpart in the reference; used by benchmarks to time the main GEMM
- * kernel apart from the B^T staging kernel that argmax calls also launch. */
+ * kernel apart from the B^T staging kernel that some argmax calls also launch. */
 
 /* on != 0: every forward call records a HIP event pair on its stream around
  * its main GEMM kernel(s).  Off by default (no events, no overhead). */
@@ -110,8 +110,9 @@ int tg_kernel_timing_read(double* total_ms, int64_t* launches);
  *   A: m x k, B: k x n, C: m x n, argmax: m x n int32 or NULL (value-only).
  * m, n, k >= 0; k == 0 yields C = tropical zero and argmax = 0
  * (core/gemm.rs:70-72 leaves the zero-initialised result untouched).
- * Uses a stream-ordered workspace allocation when argmax != NULL; see
- * tg_gemm_workspace_size / tg_gemm_ws to pass one instead.
+ * Uses a stream-ordered workspace allocation when the kernel it picks needs
+ * one (argmax with B^T staging, split K); see tg_gemm_workspace_size /
+ * tg_gemm_ws to pass one instead.
  */
 int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
             const void* A, const void* B, void* C, int32_t* argmax,

@@ -28,7 +28,8 @@ def test_more_than_one_gpu_is_refused():
 @pytest.mark.gpu
 @pytest.mark.parametrize("args", [("--config", "P", "--cpu-rows", "64"),
                                   ("--config", "C1", "--cpu-rows", "0"),
-                                  ("--config", "E1")], ids=["P", "C1", "E1"])
+                                  ("--config", "M1"), ("--config", "E1")],
+                         ids=["P", "C1", "M1", "E1"])
 def test_json_line(args):
     print(f"[case] bench.py {' '.join(args)}", flush=True)
     r = _bench(*args, "--steps", "2", "--warmup", "1")
@@ -45,6 +46,9 @@ def test_json_line(args):
         assert key in out["roofline"], key
     roof = out["roofline"]
     assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    if args[1] == "M1":  # short K: HBM-bound, GB/s against 8 TB/s
+        assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
+        assert out["argmax_consistency_check"] is True
     if args[1] == "P":
         base = out["cpu_baseline"]
         assert base["value"] > 0 and base["cores"] == 1 and base["kind"] in ("port", "reference")

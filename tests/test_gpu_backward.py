@@ -180,7 +180,7 @@ def test_autograd_finite_differences_maxplus():
             for kk in range(k):
                 ap = a.detach().clone()
                 ap[i, kk] += 1e-3
-                num = (tp.tropical_maxplus_matmul_gpu(ap, b.detach())[i, j] - c[i, j]) / 1e-3
+                num = (tp.tropical_maxplus_matmul_gpu(ap, b.detach())[i, j] - c[i, j].detach()) / 1e-3
                 assert abs(float(num) - float(ga[i, kk])) < 0.05
 
 

@@ -84,6 +84,14 @@ def test_c4_viterbi_i32_full_size():
     np.testing.assert_array_equal(am.cpu().numpy(), am_ref.astype(np.int32))
 
 
+def test_m1_short_k_full_size():
+    cfg, a, b, c, am = _run("M1", True)
+    _check_consistency("maxplus", a, b, c, am)
+    c_ref, am_ref = oracle.gemm("maxplus", a.cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(tc.bits(c.cpu().numpy()), tc.bits(c_ref))
+    np.testing.assert_array_equal(am.cpu().numpy(), am_ref.astype(np.int32))
+
+
 def test_c5_backward_full_size():
     from tropical_gemm import ops
 

@@ -4,11 +4,12 @@ Every entry point that takes a caller workspace launches kernels only (no
 allocation, no memset: buffers that must start at zero are cleared by a fill
 kernel), so a caller can capture it in a HIP graph and replay it.  The test
 captures the forward paths (direct-to-LDS tiles with B^T staging, 64x128
-tiles, split K, the K-resident kernel, the generic tiles, value-only) and both backward
-scatters, replays the graph several times with new inputs copied in and eager
-work between the replays, and checks every replay against eager calls on the
-same inputs, bit for bit (the backward too: each gradient element receives a
-single contribution, so the sum order cannot differ)."""
+tiles, split K, the K-resident kernel, the generic tiles, their exact
+short-K mode, value-only) and both backward scatters, replays the graph
+several times with new inputs copied in and eager work between the replays,
+and checks every replay against eager calls on the same inputs, bit for bit
+(the backward too: each gradient element receives a single contribution, so
+the sum order cannot differ)."""
 import ctypes
 
 import numpy as np
@@ -26,6 +27,7 @@ CASES = [
     ("split-K", "maxplus", torch.float32, 128, 4096, 128, True),
     ("K-resident", "maxplus", torch.int32, 512, 128, 128, True),
     ("generic tiles", "minplus", torch.float64, 77, 45, 93, True),
+    ("exact short K", "maxplus", torch.float32, 1000, 16, 1024, True),
     ("value-only", "maxmul", torch.float32, 256, 256, 192, False),
 ]
 

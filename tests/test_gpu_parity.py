@@ -831,3 +831,107 @@ def test_split_k_minimum_workspace_and_batches():
     for t in range(batch):
         assert_exact(cc[t * sc: t * sc + 128 * 64].reshape(128, 64),
                      aa[t * sc: t * sc + 128 * 64].reshape(128, 64), *oracle.gemm("maxplus", a3[t], b3[t]))
+
+
+# ---------------------------------------------------------------------------
+# Short K (at most 32): the tiles kernel's exact mode, which tracks the index
+# of every product (no chunk records, no resolve, no B^T staging) and writes
+# four consecutive outputs per 16-byte store where the rows allow it.
+# ---------------------------------------------------------------------------
+
+EXACT_KS = [1, 2, 5, 8, 16, 31, 32, 33]
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64", "i32", "i64"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_exact_mode_short_k(sr, dt):
+    """K up to 32 on both sides of the boundary (33 takes the chunked
+    kernels), N a multiple of 4 (vector stores) or odd (element stores),
+    random values and values in {0, 1, 2} (many maximisers per output)."""
+    rng = np.random.default_rng(300 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for k in EXACT_KS:
+        for (m, n) in [(200, 132), (77, 45), (129, 256)]:
+            for ties in (False, True):
+                print(f"[case] exact {sr} {dt} m={m} k={k} n={n} ties={ties}", flush=True)
+                if ties:
+                    a = rng.integers(0, 3, size=(m, k)).astype(dtype)
+                    b = rng.integers(0, 3, size=(k, n)).astype(dtype)
+                else:
+                    a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+                    b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+                ref = oracle.gemm(sr, a, b)
+                assert_exact(*gpu_gemm(sr, a, b, True, api="min"), *ref)
+                c, _ = gpu_gemm(sr, a, b, False)
+                assert_exact(c, None, ref[0], None)
+
+
+def test_exact_mode_special_values_and_zero_rows():
+    rng = np.random.default_rng(310)
+    m, k, n = 96, 24, 136
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a[rng.random(a.shape) < 0.2] = -np.inf
+    b[rng.random(b.shape) < 0.2] = -np.inf
+    a[3, :] = -np.inf  # never beats the zero: -inf with argmax 0
+    c, am = gpu_gemm("maxplus", a, b)
+    assert_exact(c, am, *oracle.gemm("maxplus", a, b))
+    assert np.all(np.isneginf(c[3])) and np.all(am[3] == 0)
+    ai = np.where(np.isinf(a), np.inf, a).astype(np.float32)
+    bi = np.where(np.isinf(b), np.inf, b).astype(np.float32)
+    assert_exact(*gpu_gemm("minplus", ai, bi), *oracle.gemm("minplus", ai, bi))
+    # -0 at k = 0 ties +0 later: the first one (-0, index 0) stays.
+    z = np.zeros((4, 9), np.float32)
+    z[:, 0] = -0.0
+    w = np.full((9, 8), -1.0, np.float32)
+    w[0, :] = -0.0
+    w[6, :] = 0.0
+    c, am = gpu_gemm("maxplus", z, w)
+    assert np.all(np.signbit(c)) and np.all(am == 0)
+    # Integer wraparound.
+    ia = rng.integers(2**31 - 60, 2**31 - 1, size=(70, 12)).astype(np.int32)
+    ib = rng.integers(-5, 60, size=(12, 44)).astype(np.int32)
+    for sr in tc.SEMIRINGS:
+        assert_exact(*gpu_gemm(sr, ia, ib), *oracle.gemm(sr, ia, ib))
+
+
+@pytest.mark.parametrize("dt", ["f32", "f64"])
+def test_exact_mode_strided_batches_and_misaligned_outputs(dt):
+    """Strided batches whose output stride keeps (sc = m*n + 4) or breaks
+    (m*n + 1) 16-byte alignment of each item's rows, and a C / argmax pair
+    that starts one element past an aligned address (element stores)."""
+    nat = _nat()
+    lib = nat.load()
+    rng = np.random.default_rng(320)
+    dtype = tc.NP_DTYPES[dt]
+    d = nat.DTYPE[dt]
+    batch, m, k, n = 3, 70, 20, 68
+    for gap_c in (4, 1):
+        print(f"[case] exact strided {dt} gap_c={gap_c}", flush=True)
+        sa, sb, sc = m * k + 3, k * n + 5, m * n + gap_c
+        a = tc.rng_matrix(rng, dtype, (batch * sa,), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (batch * sb,), -1000, 1000)
+        ta, tb = _dev(a), _dev(b)
+        c = torch.zeros(batch * sc, dtype=TORCH_DT[np.dtype(dtype)], device=DEV)
+        am = torch.zeros(batch * sc, dtype=torch.int32, device=DEV)
+        nat.check(lib.tg_gemm_strided_batched(0, nat.SEMIRING["maxplus"], d, 0, _p(ta), _p(tb),
+                                              _p(c), _p(am), batch, m, n, k, sa, sb, sc, None))
+        torch.cuda.synchronize()
+        c_np, am_np = c.cpu().numpy(), am.cpu().numpy()
+        for t in range(batch):
+            ref = oracle.gemm("maxplus", a[t * sa:t * sa + m * k].reshape(m, k),
+                              b[t * sb:t * sb + k * n].reshape(k, n))
+            assert_exact(c_np[t * sc:t * sc + m * n].reshape(m, n),
+                         am_np[t * sc:t * sc + m * n].reshape(m, n), *ref)
+    print(f"[case] exact misaligned output {dt}", flush=True)
+    a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+    b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+    ta, tb = _dev(a), _dev(b)
+    c = torch.zeros(m * n + 1, dtype=TORCH_DT[np.dtype(dtype)], device=DEV)
+    am = torch.zeros(m * n + 1, dtype=torch.int32, device=DEV)
+    nat.check(lib.tg_gemm(0, nat.SEMIRING["minplus"], d, 0, _p(ta), _p(tb),
+                          ctypes.c_void_p(c.data_ptr() + c.element_size()),
+                          ctypes.c_void_p(am.data_ptr() + 4), m, n, k, None))
+    torch.cuda.synchronize()
+    assert_exact(c.cpu().numpy()[1:].reshape(m, n), am.cpu().numpy()[1:].reshape(m, n),
+                 *oracle.gemm("minplus", a, b))

@@ -381,53 +381,131 @@ int run_gemm_kres(const Problem& p, hipStream_t st) {
     return TG_OK;
 }
 
-// True when the argmax problem runs on the K-resident kernel (which needs no
-// B^T workspace).
-bool uses_kres(tg_dtype dt, const Problem& p) {
-    return (dt == TG_F32 || dt == TG_I32) && p.IDX != nullptr &&
-           tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX);
+// Argmax problems with K up to this run the generic tiles kernel in its exact
+// mode (per-product index tracking, no resolve, no B^T staging): at short K
+// the chunked kernels' resolve, which re-reads A and B^T windows per output,
+// costs several times the main loop.
+constexpr int64_t kExactMaxK = 32;
+// Argmax problems that reach the generic tiles kernel (no direct-to-LDS or
+// K-resident kernel takes them) run its exact mode up to this K: 4 VALU ops
+// per product against the chunked mode's ~2 plus its resolve.  Crossovers
+// measured on MI355X (MaxPlus, M = N = 4096): f32 near K = 480, f64 near
+// K = 700, i64 near K = 4096 (its 64-bit compare costs as much as the add).
+template <typename T>
+constexpr int64_t exact_tiles_max_k() {
+    return sizeof(T) == 4 ? 384 : std::is_same<T, int64_t>::value ? 2048 : 512;
+}
+
+// The kernel a problem runs on.
+enum class Path { KRES8, KRES, DL_8_16, DL_4_8, DL_4_16, DL_4_32, TILES_EXACT, TILES_CHUNKED, TILES };
+
+struct Plan {
+    Path path = Path::TILES;
+    int splits = 1;
+};
+
+// True when the path reads the workspace: B^T staging for the resolve of the
+// chunked argmax kernels, and split-K partials.
+bool uses_workspace(const Plan& pl, bool argmax) {
+    switch (pl.path) {
+        case Path::KRES8:
+        case Path::KRES:
+        case Path::TILES_EXACT:
+        case Path::TILES: return false;
+        case Path::TILES_CHUNKED: return true;
+        default: return argmax || pl.splits > 1;
+    }
+}
+
+// Chooses the kernel.  ws_bytes limits split K (the partials live in the
+// workspace).
+template <int SR, typename T>
+Plan plan_typed(const Problem& p, size_t ws_bytes) {
+    Plan pl;
+    const bool argmax = p.IDX != nullptr;
+    const bool exact = argmax && p.K <= kExactMaxK;
+    if constexpr (sizeof(T) == 4) {
+        if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL) {
+            if (argmax && tg::kres8_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::KRES8;
+                return pl;
+            }
+        }
+        if (argmax && tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+            pl.path = Path::KRES;
+            return pl;
+        }
+        if (!exact) {
+            // Direct-to-LDS kernels (value-only, or argmax beyond the exact
+            // range).  Split K when the problem makes too few 64 x 64 tiles
+            // and the workspace holds the partials (tg_gemm_workspace_size
+            // includes them).
+            const tg_dtype dt = std::is_same<T, float>::value ? TG_F32 : TG_I32;
+            int splits = tg::dl_splits(p.M, p.N, p.K, p.batch);
+            if (splits > 1 && ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, splits).total > ws_bytes)
+                splits = 1;
+            const int64_t ks = p.K / splits;
+            // Argmax chunk length.  The bookkeeping costs 2 VALU ops per output
+            // per chunk (2K/CL); the resolve re-reads one chunk's A-row and
+            // B^T-row segments per output from L2 and recomputes them, which
+            // costs more than its ~4 ops per product suggest.  Measured on
+            // MI355X (f32 MaxPlus, slices of 256 .. 4096 k): CL = 8 is fastest
+            // up to 512 k per slice, CL = 16 above (CL = 32 is 4-18% slower
+            // everywhere).
+            const int cl = !argmax ? 32 : ks <= 512 ? 8 : 16;
+            // 64 x 128 tiles for argmax problems big enough that the last
+            // round of 768 resident workgroups is a small share of the work
+            // (their main loop is the faster one); 64 x 64 tiles otherwise
+            // (value-only runs four workgroups per CU, small problems get
+            // twice the tiles).
+            const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
+                              (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
+            pl.splits = splits;
+            if (wide && tg::dl_fits<8, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_8_16;
+                pl.splits = 1;
+                return pl;
+            }
+            if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_4_8;
+                return pl;
+            }
+            if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_4_16;
+                return pl;
+            }
+            if (cl == 32 && tg::dl_fits<4, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_4_32;
+                return pl;
+            }
+            pl.splits = 1;
+        }
+    }
+    if (!argmax)
+        pl.path = Path::TILES;
+    else if (exact || p.K <= exact_tiles_max_k<T>())
+        pl.path = Path::TILES_EXACT;
+    else
+        pl.path = Path::TILES_CHUNKED;
+    return pl;
 }
 
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
+    const Plan pl = plan_typed<SR, T>(p, ws_bytes);
     if constexpr (sizeof(T) == 4) {
-        if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL) {
-            if (p.IDX != nullptr &&
-                tg::kres8_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-                return run_gemm_kres8<SR>(p, st);
+        switch (pl.path) {
+            case Path::KRES8:
+                if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL)
+                    return run_gemm_kres8<SR>(p, st);
+                break;
+            case Path::KRES: return run_gemm_kres<SR, T>(p, st);
+            case Path::DL_8_16: return run_gemm_dl<SR, T, 8, 16>(p, ws, 1, st);
+            case Path::DL_4_8: return run_gemm_dl<SR, T, 4, 8>(p, ws, pl.splits, st);
+            case Path::DL_4_16: return run_gemm_dl<SR, T, 4, 16>(p, ws, pl.splits, st);
+            case Path::DL_4_32: return run_gemm_dl<SR, T, 4, 32>(p, ws, pl.splits, st);
+            default: break;
         }
-        if (p.IDX != nullptr &&
-            tg::kres_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_kres<SR, T>(p, st);
-        const bool argmax = p.IDX != nullptr;
-        const tg_dtype dt = std::is_same<T, float>::value ? TG_F32 : TG_I32;
-        // Split K when the problem makes too few 64 x 64 tiles and the
-        // workspace holds the partials (tg_gemm_workspace_size includes them).
-        int splits = tg::dl_splits(p.M, p.N, p.K, p.batch);
-        if (splits > 1 && ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, splits).total > ws_bytes)
-            splits = 1;
-        const int64_t ks = p.K / splits;
-        // Argmax chunk length.  The bookkeeping costs 2 VALU ops per output per
-        // chunk (2K/CL); the resolve re-reads one chunk's A-row and B^T-row
-        // segments per output from L2 and recomputes them, which costs more
-        // than its ~4 ops per product suggest.  Measured on MI355X (f32
-        // MaxPlus, slices of 256 .. 4096 k): CL = 8 is fastest up to 512 k
-        // per slice, CL = 16 above (CL = 32 is 4-18% slower everywhere).
-        const int cl = !argmax ? 32 : ks <= 512 ? 8 : 16;
-        // 64 x 128 tiles for argmax problems big enough that the last round
-        // of 768 resident workgroups is a small share of the work (their
-        // main loop is the faster one); 64 x 64 tiles otherwise (value-only
-        // runs four workgroups per CU, small problems get twice the tiles).
-        const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
-                          (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
-        if (wide && tg::dl_fits<8, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 8, 16>(p, ws, 1, st);
-        if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 8>(p, ws, splits, st);
-        if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 16>(p, ws, splits, st);
-        if (cl == 32 && tg::dl_fits<4, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX))
-            return run_gemm_dl<SR, T, 4, 32>(p, ws, splits, st);
     }
     using Cfg = tg::TileCfg<T>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
@@ -449,7 +527,18 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
         T* Cz = C + z0 * p.sC;
         int32_t* Iz = argmax ? p.IDX + z0 * p.sC : nullptr;
         dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
-        if (argmax) {
+        if (pl.path == Path::TILES_EXACT) {
+            KernelTimer timer(st);
+            if (vec)
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true, true>), grid, dim3(256), 0,
+                                   st, Az, Bz, nullptr, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
+            else
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false, true>), grid, dim3(256), 0,
+                                   st, Az, Bz, nullptr, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                                   int(tiles_m), int(tiles_n));
+            TG_HIP(hipGetLastError());
+        } else if (pl.path == Path::TILES_CHUNKED) {
             // B^T staging for the argmax epilogue (dense, batch stride K*N).
             T* BT = static_cast<T*>(ws);
             const int64_t sBT = p.K * p.N;
@@ -496,6 +585,26 @@ int run_gemm_sr(tg_dtype dt, const Problem& p, void* ws, size_t ws_bytes, hipStr
         case TG_I64: return run_gemm_typed<SR, int64_t>(p, ws, ws_bytes, st);
     }
     return fail(TG_ERR_INVALID_ARGUMENT, "bad dtype");
+}
+
+template <int SR>
+Plan plan_sr(tg_dtype dt, const Problem& p, size_t ws_bytes) {
+    switch (dt) {
+        case TG_F32: return plan_typed<SR, float>(p, ws_bytes);
+        case TG_F64: return plan_typed<SR, double>(p, ws_bytes);
+        case TG_I32: return plan_typed<SR, int32_t>(p, ws_bytes);
+        case TG_I64: return plan_typed<SR, int64_t>(p, ws_bytes);
+    }
+    return Plan{};
+}
+
+Plan plan_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, size_t ws_bytes) {
+    switch (sr) {
+        case TG_MAXPLUS: return plan_sr<tg::SR_MAXPLUS>(dt, p, ws_bytes);
+        case TG_MINPLUS: return plan_sr<tg::SR_MINPLUS>(dt, p, ws_bytes);
+        case TG_MAXMUL: return plan_sr<tg::SR_MAXMUL>(dt, p, ws_bytes);
+    }
+    return Plan{};
 }
 
 int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, size_t ws_bytes,
@@ -607,8 +716,11 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
         return fail(TG_ERR_INVALID_ARGUMENT, "internal: workspace size below K x N");
     void* work = ws;
     bool own = false;
-    if (!ws_given && !uses_kres(dt, p)) {
+    if (!ws_given) {
+        // Allocate the full workspace only for the kernels that read it.
         ws_bytes = workspace_bytes_for(dt, batch, m, n, k, with_argmax);
+        if (ws_bytes > 0 && !uses_workspace(plan_gemm(sr, dt, p, ws_bytes), with_argmax))
+            ws_bytes = 0;
         if (ws_bytes > 0) {
             TG_HIP(hipMallocAsync(&work, ws_bytes, st));
             own = true;

@@ -96,9 +96,13 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //   VEC          : K and N are multiples of 16/sizeof(T) and A, B, BT are
 //                  16-byte aligned, so tiles and argmax windows use 16-byte
 //                  global loads.
+//   EXACT        : (with ARGMAX) every product updates (value, index) on a
+//                  strict improvement, in k order: no chunk records, no
+//                  resolve and no B^T.  For short K, where the resolve's
+//                  re-reads of A and B^T would outweigh the main loop.
 // grid = (tiles_m * tiles_n, 1, batch), block = 256.
 // ---------------------------------------------------------------------------
-template <int SR, typename T, bool ARGMAX, bool VEC>
+template <int SR, typename T, bool ARGMAX, bool VEC, bool EXACT = false>
 __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
@@ -111,6 +115,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     constexpr int NVB = BK * BN / VW / TG_THREADS;  // 16-byte vectors of B per thread
     static_assert(NVA >= 1 && NVB >= 1, "tile too small for the block");
     static_assert(TM % 4 == 0 && TN % 4 == 0, "micro-tile must be made of 4-wide groups");
+    static_assert(ARGMAX || !EXACT, "EXACT is an argmax mode");
 
     __shared__ __align__(16) T As[2][BK][BM + PAD];
     __shared__ __align__(16) T Bs[2][BK][BN + PAD];
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     C += z * sC;
     if (ARGMAX) {
         IDX += z * sC;
-        BT += z * (N * K);
+        if (!EXACT) BT += z * (N * K);
     }
 
     // ---- global -> register staging ------------------------------------
@@ -195,7 +200,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
 
     // ---- accumulators ------------------------------------------------------
     // acc: running value; ch: last chunk that strictly improved it (-1: none,
-    // i.e. the tropical zero was never beaten).
+    // i.e. the tropical zero was never beaten).  EXACT: ch is the argmax
+    // itself, 0 until a product beats the zero.
     T acc[TM][TN];
     int32_t ch[TM][TN];
 #pragma unroll
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             acc[i][j] = tzero<SR, T>();
-            ch[i][j] = -1;
+            ch[i][j] = EXACT ? 0 : -1;
         }
 
     auto load_frag = [&](int buf, int kk, T (&a)[TM], T (&b)[TN]) {
@@ -231,6 +237,29 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         const int64_t k0 = t * BK;
         if (t + 1 < ntiles) load_tiles(k0 + BK);
 
+        if constexpr (EXACT) {
+            // Every product in k order; strict improvement keeps the first k.
+            auto step = [&](int kk) {
+                T a0[TM], b0[TN];
+                load_frag(buf, kk, a0, b0);
+                const int32_t kg = int32_t(k0 + kk);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const T p = tmul<SR, T>(a0[i], b0[j]);
+                        const bool better = tbetter<SR, T>(p, acc[i][j]);
+                        acc[i][j] = better ? p : acc[i][j];
+                        ch[i][j] = better ? kg : ch[i][j];
+                    }
+            };
+            const int kcnt = k0 + BK <= K ? BK : int(K - k0);
+#pragma unroll 4
+            for (int kk = 0; kk < kcnt; ++kk) step(kk);
+            if (t + 1 < ntiles) store_tiles(buf ^ 1);
+            __syncthreads();
+            continue;
+        }
         // Chunk maximum (minimum for MinPlus) over this chunk's products.
         T cm[TM][TN];
         if (k0 + BK <= K) {
@@ -292,15 +321,57 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     }
 
     // ---- epilogue ------------------------------------------------------------
-    if constexpr (!ARGMAX) {
+    if constexpr (!ARGMAX || EXACT) {
+        // Values (and EXACT indices) as they stand.  Each thread's columns
+        // come in groups of 4 consecutive ones: one 16-byte store per group
+        // and array when the rows are 16-byte aligned, element stores at the
+        // ragged right edge or otherwise.
+        const bool vec_out = N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
+                             (!ARGMAX || (reinterpret_cast<uintptr_t>(IDX) & 15u) == 0);
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
             if (gr >= M) continue;
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
-                if (gc < N) C[gr * N + gc] = acc[i][j];
+            for (int g = 0; g < TN / 4; ++g) {
+                const int64_t gc = col0 + g * 64 + tx * 4;
+                if (vec_out && gc + 3 < N) {
+                    T cv[4];
+                    int32_t iv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        cv[e] = acc[i][g * 4 + e];
+                        iv[e] = ch[i][g * 4 + e];
+                    }
+                    static_assert(sizeof(cv) % 16 == 0, "4 values make whole 16-byte vectors");
+#pragma unroll
+                    for (int w = 0; w < int(sizeof(cv)) / 16; ++w) {
+                        if constexpr (!ARGMAX) {
+                            // Value-only: non-temporal (streaming) stores,
+                            // 8-15% faster at short K on MI355X; with argmax
+                            // they were 10-20% slower, so plain stores there.
+                            typedef int v4i_t __attribute__((ext_vector_type(4)));
+                            v4i_t x;
+                            __builtin_memcpy(&x, reinterpret_cast<const char*>(cv) + 16 * w, 16);
+                            __builtin_nontemporal_store(
+                                x, reinterpret_cast<v4i_t*>(C + gr * N + gc) + w);
+                        } else {
+                            reinterpret_cast<Vec16<T>*>(C + gr * N + gc)[w] =
+                                reinterpret_cast<const Vec16<T>*>(cv)[w];
+                        }
+                    }
+                    if constexpr (ARGMAX)
+                        *reinterpret_cast<Vec16<int32_t>*>(IDX + gr * N + gc) =
+                            *reinterpret_cast<const Vec16<int32_t>*>(iv);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (gc + e < N) {
+                            C[gr * N + gc + e] = acc[i][g * 4 + e];
+                            if constexpr (ARGMAX) IDX[gr * N + gc + e] = ch[i][g * 4 + e];
+                        }
+                    }
+                }
             }
         }
     } else {

@@ -10,6 +10,8 @@ the host) to the CPU oracle.  Nothing here reads the reference.
     C3  MaxMul f32 value-only, M=8192 K=2048 N=4096, entries in (0,1]
     C4  MaxPlus i32 M=262144 K=128 N=128 with argmax; A in [-1000,1000], B in [-50,0]
     C5  P forward, then backward with dC ~ N(0,1)
+    M1  MaxPlus f32 M=65536 K=8 N=2048 with argmax, N(0,1): short K, bound by
+        HBM (the 0.5 GB output and argmax writes), not by the VALU
     E1  tropical einsum "jik,lkj,lm->im", MaxPlus f32, N(0,1): i = l = m = 2048,
         j = 32, k = 64 (two 2048^3 contractions after two permutations)
 """
@@ -27,6 +29,7 @@ CONFIGS = {
     "C4": dict(semiring="maxplus", dtype="i32", m=262144, k=128, n=128, argmax=True),
     "C5": dict(semiring="maxplus", dtype="f32", m=4096, k=4096, n=4096, argmax=True,
                backward=True),
+    "M1": dict(semiring="maxplus", dtype="f32", m=65536, k=8, n=2048, argmax=True, bound="hbm"),
 }
 
 
@@ -44,7 +47,7 @@ def make_inputs(name: str, device="cuda", scale: float = 1.0):
     m = max(1, int(cfg["m"] * scale))
     k = cfg["k"] if name == "C4" else max(1, int(cfg["k"] * scale))
     n = cfg["n"] if name == "C4" else max(1, int(cfg["n"] * scale))
-    if name in ("P", "C1", "C5"):
+    if name in ("P", "C1", "C5", "M1"):
         a = torch.randn(m, k, generator=_gen(device, idx, 0), device=device)
         b = torch.randn(k, n, generator=_gen(device, idx, 1), device=device)
     elif name == "C2":
