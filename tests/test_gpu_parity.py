@@ -623,16 +623,16 @@ def _strided_batched(sr, items, gap_a=24, gap_c=40):
     return out
 
 
-# The K-resident kernel with 64 x 128 tiles (i32 MaxPlus/MinPlus, N a
-# multiple of 128): batch items change the resident B panel; a row tile that
-# leaves the f32-key range turns the B panel raw for the chunked path and the
-# next tile turns it back into keys; a batch item whose B panel is out of
-# range runs every tile chunked.
+# The 64 x 128 K-resident kernel (i32 MaxPlus/MinPlus, N a multiple of
+# 128): batch items change the resident B panel; a row tile that leaves the
+# f32-key range turns the B panel raw for the chunked path and the next tile
+# turns it back into keys; a batch item whose B panel is out of range runs
+# every tile chunked.
 @pytest.mark.parametrize("sr", ["maxplus", "minplus"])
 def test_k_resident_wide_tiles(sr):
     rng = np.random.default_rng(57 + (sr == "minplus"))
     for (m, k, n, batch) in [(256, 64, 256, 1), (512, 96, 128, 3), (384, 128, 384, 2),
-                             (4096, 128, 128, 2)]:
+                             (4096, 128, 128, 2), (4160, 128, 128, 2)]:
         print(f"[case] k-resident 64x128 {sr} m={m} k={k} n={n} batch={batch}", flush=True)
         items = []
         for t in range(batch):
@@ -650,6 +650,30 @@ def test_k_resident_wide_tiles(sr):
                              size=(k, n)).astype(np.int32)
             for api in ("alloc", "min"):
                 assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus"])
+def test_k_resident_several_tiles_per_workgroup(sr):
+    """2048 row tiles over the persistent grid (several per workgroup):
+    tiles that fail the key-range vote next to tiles that pass it, in both
+    orders within one workgroup, plus a batch of two with the second item's B
+    panel out of range."""
+    rng = np.random.default_rng(59 + (sr == "minplus"))
+    m, k, n = 131072, 128, 128
+    a = rng.integers(-1000, 1001, size=(m, k))
+    b = rng.integers(-50, 1, size=(k, n))
+    for row in (70, 128 * 513 + 5, 128 * 900 + 127, 128 * 901):
+        a[row, row % k] = -40000
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    print(f"[case] k-resident {sr} m={m} scattered out-of-range rows", flush=True)
+    assert_exact(*gpu_gemm(sr, a, b, True, api="min"), *oracle.gemm(sr, a, b))
+    b2 = b.copy()
+    b2[100, 0] = 1 << 17
+    items = [(a[:65536], b), (a[65536:], b2)]
+    print(f"[case] k-resident {sr} batch of two, second B out of range", flush=True)
+    for (c, am), (x, y) in zip(_strided_batched(sr, items), items):
+        assert_exact(c, am, *oracle.gemm(sr, x, y))
 
 
 # Short-K i32 argmax over ragged and full-tile shapes (K in {32, 64, 96,
