@@ -517,8 +517,44 @@ __global__ __launch_bounds__(256) void tg_fill_zero(unsigned char* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Floating-point add into LDS.  On gfx950 ds_add_f32 takes about three
+// clocks per distinct address in a wave (measured: 0.33 lane-updates per
+// clock and CU with scattered bins) but merges lanes that share an address,
+// while a compare-and-swap of the bits runs at ~2.4 when bins rarely collide
+// and costs more than the hardware add when most lanes share a few bins.  So
+// with cas = true f32 tries one CAS and the lanes whose CAS lost a race
+// (another lane or wave changed the bin first) fall back to the hardware add;
+// callers pass cas = false for waves whose indices repeat a lot
+// (repetitive_wave).  Either way the sum is the same set of IEEE additions in
+// some order, as with the plain atomic.  f64 always uses ds_add_f64, which
+// showed no such penalty.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void lds_add(T* p, T v, bool cas) {
+    if constexpr (sizeof(T) == 4) {
+        if (cas) {
+            uint32_t* q = reinterpret_cast<uint32_t*>(p);
+            const uint32_t old = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (atomicCAS(q, old, __float_as_uint(__uint_as_float(old) + v)) == old) return;
+        }
+    }
+    atomicAdd(p, v);
+}
+
+// True when more than 1/8 of the wave's lanes share their index with lane ^ 1
+// or lane ^ 2 (a few bins take most of the wave: the argmax of a row often
+// repeats, one distinct index per 64 lanes in the worst case).  Every lane
+// calls it (all lanes hold a defined index).
+__device__ __forceinline__ bool repetitive_wave(int32_t k) {
+    // DPP quad permutations [1,0,3,2] and [2,3,0,1] (VALU, no LDS traffic).
+    const int32_t k1 = __builtin_amdgcn_update_dpp(k, k, 0xB1, 0xF, 0xF, true);
+    const int32_t k2 = __builtin_amdgcn_update_dpp(k, k, 0x4E, 0xF, 0xF, true);
+    return __popcll(__ballot(k == k1)) + __popcll(__ballot(k == k2)) > 16;
+}
+
+// ---------------------------------------------------------------------------
 // grad_A rows: one workgroup per (row i, batch z); the row of grad_A (K
-// values) is accumulated in LDS with ds_add and written out whole, so no
+// values) is accumulated in LDS (lds_add) and written out whole, so no
 // global atomics and no separate zero fill are needed.
 //   MULT=true: MaxMul rule, g *= B[kk, j]  (OTHER = B, row-major K x N).
 // grid = (M, 1, batch), block = 256, dynamic LDS = K * sizeof(T).
@@ -553,10 +589,11 @@ __global__ __launch_bounds__(256) void tg_backward_rows(const T* __restrict__ G,
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            const bool cas = !repetitive_wave(kk[u]);
             if (kk[u] >= 0 && int64_t(kk[u]) < K) {
                 T v = g[u];
                 if (MULT) v = v * OTHER[int64_t(kk[u]) * N + j0 + u * 256 + threadIdx.x];
-                atomicAdd(&row[kk[u]], v);
+                lds_add(&row[kk[u]], v, cas);
             }
         }
     }
@@ -667,7 +704,9 @@ __global__ __launch_bounds__(512) void tg_backward_cols_lds(const T* __restrict_
                 const int64_t e = e0 + u * 512 + threadIdx.x;
                 T v = g[u];
                 if (MULT) v = v * OTHER[(e >> bj_log2) * K + kk[u]];
-                atomicAdd(&acc[int64_t(kk[u]) * BJ + (e & (BJ - 1))], v);
+                // Neighbouring lanes hold neighbouring columns, so their
+                // bins differ even where the argmax repeats: always CAS.
+                lds_add(&acc[int64_t(kk[u]) * BJ + (e & (BJ - 1))], v, true);
             }
         }
     }
