@@ -1,8 +1,8 @@
 """Seeded GPU fuzz of the forward entry points against the oracle.
 
-Random problems aimed at every dispatch path (generic tiles with ragged edges,
-direct-to-LDS full tiles, wide tiles, the K-resident kernel with its three
-integer paths, split K) over all dtypes, semirings and both layouts, single
+Random problems aimed at every dispatch path (generic tiles with ragged edges
+and their exact short-K mode, direct-to-LDS full tiles, wide tiles, the
+K-resident kernel with its three integer paths, split K) over all dtypes, semirings and both layouts, single
 and strided-batched, with a caller workspace or the library's own.  Every
 output, the gaps between strided outputs and the workspace are surrounded by
 guard bytes that must come back untouched, and every result must equal the
