@@ -78,28 +78,53 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def run_cpu_baseline(rows: int) -> dict:
-    """Single-thread reference-algorithm restatement on a row slab of P."""
+# Rows of each configuration's CPU-baseline sample outside P (P: --cpu-rows):
+# about 0.5-4 s of single-core work.  C1 and C4 run whole; M1's short K makes
+# the reference's blocked loops slow (0.07 GOP/s), hence its small slab.
+CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096}
+
+
+def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> dict:
+    """Single-thread restatement of the reference CPU algorithm for this
+    configuration, timed on the first ``rows`` rows of the same inputs:
+    argmax configurations run the reference's argmax path (BLIS PORTABLE
+    tiling, 4x4 scalar microkernel); value-only f32 ones (and C1's
+    value-only line) its AVX2 path (F32_AVX2 tiling, 8x8 microkernel)."""
     import numpy as np
 
     from oracle import oracle
 
-    rng = np.random.default_rng(0x7E0000)
-    k = n = 4096
-    a = rng.standard_normal((rows, k)).astype(np.float32)
-    b = rng.standard_normal((k, n)).astype(np.float32)
+    m, k = a.shape
+    n = b.shape[1]
+    rows = max(1, min(rows, m))
+    ha = a[:rows].cpu().numpy()
+    hb = b.cpu().numpy()
+    sr = cfg["semiring"]
+    if cfg["argmax"] and not value_only:
+        fn, algo = oracle.portable_argmax, ("argmax algorithm (BLIS PORTABLE tiling, 4x4 scalar "
+                                            "microkernel)")
+    elif ha.dtype == np.float32:
+        fn, algo = oracle.avx2_gemm_f32, ("value-only algorithm (BLIS F32_AVX2 tiling, AVX2 8x8 "
+                                          "microkernel)")
+    else:
+        raise ValueError("no CPU baseline restated for this configuration")
     t0 = time.perf_counter()
-    oracle.portable_argmax_f32("maxplus", a, b)
+    fn(sr, ha, hb)
     dt = time.perf_counter() - t0
+    what = "the whole product" if rows == m else f"a {rows}-row slab"
     return {
         "value": round(2.0 * rows * n * k / dt / 1e9, 3),
         "unit": "GOP/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{rows}x4096x4096 row slab of P (MaxPlus f32 +argmax), reference CPU argmax "
-                   f"algorithm (BLIS PORTABLE tiling, 4x4 scalar microkernel) restated in C, "
-                   f"1 thread, {dt:.1f} s on {cpu_model()}"),
+        "sample": (f"{what} ({rows}x{k}x{n}, {sr} {ha.dtype}) of this configuration's inputs, "
+                   f"reference CPU {algo} restated in C, 1 thread, {dt:.1f} s on {cpu_model()}"),
     }
+
+
+def cpu_rows_for(name: str, p_rows: int) -> int:
+    """P uses --cpu-rows; the others their CPU_ROWS sample."""
+    return p_rows if name == "P" else CPU_ROWS[name]
 
 
 def run_einsum(args, lib, dev) -> int:
@@ -216,7 +241,8 @@ def main() -> int:
     ap.add_argument("--config", default="P",
                     choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
-                    help="rows of the CPU-baseline slab (0 skips the CPU baseline)")
+                    help="rows of P's CPU-baseline slab (0 skips the CPU baseline of every "
+                         "configuration)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB once (a known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -386,9 +412,14 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize(dev)
         out["copy_calibration_bytes"] = args.copy_mib << 20
-    if args.cpu_rows > 0 and args.config == "P":
-        out["cpu_baseline"] = run_cpu_baseline(args.cpu_rows)
+    if args.cpu_rows > 0:
+        rows = cpu_rows_for(args.config, args.cpu_rows)
+        out["cpu_baseline"] = run_cpu_baseline(cfg, a, b, rows)
         out["gpu_vs_cpu_baseline"] = round(gops / out["cpu_baseline"]["value"], 1)
+        if args.config == "C1":
+            # The reference's value-only CPU path on the same product (its
+            # headline CPU number is this path at n = 1024).
+            out["cpu_baseline_value_only"] = run_cpu_baseline(cfg, a, b, rows, value_only=True)
     print(json.dumps(out), flush=True)
     return 0
 

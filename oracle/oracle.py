@@ -57,8 +57,12 @@ def _load():
             fn = getattr(lib, name)
             fn.argtypes = [vp, vp, vp, vp, i64, i64, i64]
             fn.restype = None
-        lib.tgo_portable_argmax_f32.argtypes = [ctypes.c_int, vp, vp, vp, vp, i64, i64, i64]
-        lib.tgo_portable_argmax_f32.restype = ctypes.c_int
+        for name in ("tgo_portable_argmax_f32", "tgo_portable_argmax_i32"):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.c_int, vp, vp, vp, vp, i64, i64, i64]
+            fn.restype = ctypes.c_int
+        lib.tgo_avx2_gemm_f32.argtypes = [ctypes.c_int, vp, vp, vp, i64, i64, i64]
+        lib.tgo_avx2_gemm_f32.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -132,17 +136,41 @@ def backward_b(grad_c: np.ndarray, argmax: np.ndarray, k: int, a: np.ndarray | N
     return out
 
 
-def portable_argmax_f32(semiring: str, a: np.ndarray, b: np.ndarray):
+def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
     """Single-thread restatement of the reference CPU argmax path (BLIS
-    PORTABLE tiling + 4x4 scalar microkernel); used as the timed baseline."""
+    PORTABLE tiling + 4x4 scalar microkernel) for float32 or int32 operands;
+    used as the timed baseline."""
+    dt = np.dtype(a.dtype)
+    if dt not in (np.dtype(np.float32), np.dtype(np.int32)):
+        raise ValueError(f"portable baseline restated for float32 and int32, got {dt}")
+    a = np.ascontiguousarray(a, dtype=dt)
+    b = np.ascontiguousarray(b, dtype=dt)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), dtype=dt)
+    am = np.empty((m, n), dtype=np.uint32)
+    fn = _load().tgo_portable_argmax_f32 if dt == np.float32 else _load().tgo_portable_argmax_i32
+    rc = fn(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), _ptr(am), m, n, k)
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return c, am
+
+
+def portable_argmax_f32(semiring: str, a: np.ndarray, b: np.ndarray):
+    """float32 form of ``portable_argmax``."""
+    return portable_argmax(semiring, np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
+
+
+def avx2_gemm_f32(semiring: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Single-thread restatement of the reference CPU value-only f32 path
+    (BLIS F32_AVX2 tiling + AVX2 8x8 microkernel); used as the timed
+    baseline of value-only configurations."""
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)
     m, k = a.shape
     n = b.shape[1]
     c = np.empty((m, n), dtype=np.float32)
-    am = np.empty((m, n), dtype=np.uint32)
-    rc = _load().tgo_portable_argmax_f32(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), _ptr(am),
-                                         m, n, k)
+    rc = _load().tgo_avx2_gemm_f32(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), m, n, k)
     if rc != 0:
         raise ValueError("oracle rejected arguments")
-    return c, am
+    return c

@@ -30,13 +30,20 @@
  *     pthreads.  Results are therefore identical to the reference CPU path
  *     for every non-NaN input (NaN handling also follows the select rule).
  *
- *  2. tgo_portable_argmax_* : the CPU BASELINE used for timing.  A faithful
- *     single-thread restatement of the reference's argmax path: BLIS 5-loop
- *     with TilingParams::PORTABLE (MC=NC=64, KC=256, MR=NR=4;
- *     core/tiling.rs:39-45), pack_a/pack_b (core/packing.rs:46-161) and the
- *     4x4 scalar microkernel with k_offset (core/kernel.rs:119-167).
- *     Its results equal the oracle's; it exists so the timed number reflects
- *     the reference's algorithm, not the oracle's vectorised loop.
+ *  2. tgo_portable_argmax_{f32,i32} and tgo_avx2_gemm_f32 : the CPU
+ *     BASELINES used for timing.  Faithful single-thread restatements of the
+ *     reference's two CPU paths:
+ *       argmax (every dtype): BLIS 5-loop with TilingParams::PORTABLE
+ *       (MC=NC=64, KC=256, MR=NR=4; core/tiling.rs:39-45), pack_a/pack_b
+ *       (core/packing.rs:46-161) and the 4x4 scalar microkernel with
+ *       k_offset (core/kernel.rs:119-167);
+ *       value-only f32: the same 5-loop with TilingParams::F32_AVX2 (MC=NC=
+ *       256, KC=512, MR=NR=8) and the AVX2 8x8 microkernel
+ *       (simd/kernels/avx2.rs), which the reference dispatches to on AVX2 and
+ *       AVX-512 hosts alike (simd/dispatch.rs).
+ *     Their results equal the oracle's on ordinary data; they exist so the
+ *     timed numbers reflect the reference's algorithms, not the oracle's
+ *     vectorised loop.
  *
  * Build: oracle/Makefile (gcc -O3 -mavx2 -mfma -ffp-contract=off, no
  * fast-math, so every float op is the single IEEE op the reference performs).
@@ -243,96 +250,215 @@ TGO_BACKWARD_B(tgo_backward_b_f64, double)
 #define P_MR 4
 #define P_NR 4
 
-/* pack_a: mr-row panels, k-major inside a panel, pad rows with scalar 0. */
-static void pack_a_f32(int64_t mc, int64_t kc, const float* a, int64_t lda, float* packed) {
+/* The portable path for one scalar type T (suffix S): pack_a (mr-row
+ * panels, k-major inside a panel, rows padded with scalar 0), pack_b
+ * (nr-column panels, k-major, columns padded with 0), the 4x4 microkernel
+ * with argmax (load (acc, idx) from C/argmax, visit k = k_offset + p
+ * ascending with the CPU select rule, store back) and the 5-loop driver.
+ * Row-major A (M x K), B (K x N); C/argmax are initialised to tropical zero
+ * / 0 exactly as GemmWithArgmax::new does (core/argmax.rs:24-33). */
+#define TGO_PORTABLE(T, S, ZERO, MUL)                                                           \
+    static void pack_a_##S(int64_t mc, int64_t kc, const T* a, int64_t lda, T* packed) {        \
+        int64_t p = 0;                                                                          \
+        for (int64_t r0 = 0; r0 < mc; r0 += P_MR)                                               \
+            for (int64_t col = 0; col < kc; ++col)                                              \
+                for (int64_t ro = 0; ro < P_MR; ++ro) {                                         \
+                    const int64_t row = r0 + ro;                                                \
+                    packed[p++] = row < mc ? a[row * lda + col] : (T)0;                         \
+                }                                                                               \
+    }                                                                                           \
+    static void pack_b_##S(int64_t kc, int64_t nc, const T* b, int64_t ldb, T* packed) {        \
+        int64_t p = 0;                                                                          \
+        for (int64_t c0 = 0; c0 < nc; c0 += P_NR)                                               \
+            for (int64_t row = 0; row < kc; ++row)                                              \
+                for (int64_t co = 0; co < P_NR; ++co) {                                         \
+                    const int64_t col = c0 + co;                                                \
+                    packed[p++] = col < nc ? b[row * ldb + col] : (T)0;                         \
+                }                                                                               \
+    }                                                                                           \
+    static void micro_argmax_##S(int sr, int64_t mr, int64_t nr, int64_t kc, int64_t k_offset,  \
+                                 const T* pa, const T* pb, T* c, uint32_t* am, int64_t ldc) {   \
+        T acc[P_MR][P_NR];                                                                      \
+        uint32_t idx[P_MR][P_NR];                                                               \
+        for (int64_t i = 0; i < P_MR; ++i)                                                      \
+            for (int64_t j = 0; j < P_NR; ++j) {                                                \
+                acc[i][j] = ZERO(sr);                                                           \
+                idx[i][j] = 0;                                                                  \
+            }                                                                                   \
+        for (int64_t i = 0; i < mr; ++i)                                                        \
+            for (int64_t j = 0; j < nr; ++j) {                                                  \
+                acc[i][j] = c[i * ldc + j];                                                     \
+                idx[i][j] = am[i * ldc + j];                                                    \
+            }                                                                                   \
+        for (int64_t p = 0; p < kc; ++p) {                                                      \
+            const uint32_t cur = (uint32_t)(k_offset + p);                                      \
+            for (int64_t i = 0; i < mr; ++i) {                                                  \
+                const T av = pa[p * P_MR + i];                                                  \
+                for (int64_t j = 0; j < nr; ++j) {                                              \
+                    const T prod = MUL(sr, av, pb[p * P_NR + j]);                               \
+                    const int keep =                                                            \
+                        sr == TGO_MINPLUS ? (acc[i][j] <= prod) : (acc[i][j] >= prod);          \
+                    if (!keep) {                                                                \
+                        acc[i][j] = prod;                                                       \
+                        idx[i][j] = cur;                                                        \
+                    }                                                                           \
+                }                                                                               \
+            }                                                                                   \
+        }                                                                                       \
+        for (int64_t i = 0; i < mr; ++i)                                                        \
+            for (int64_t j = 0; j < nr; ++j) {                                                  \
+                c[i * ldc + j] = acc[i][j];                                                     \
+                am[i * ldc + j] = idx[i][j];                                                    \
+            }                                                                                   \
+    }                                                                                           \
+    int tgo_portable_argmax_##S(int sr, const T* A, const T* B, T* C, uint32_t* argmax,         \
+                                int64_t M, int64_t N, int64_t K) {                              \
+        if (sr < 0 || sr > 2 || M < 0 || N < 0 || K < 0) return -1;                             \
+        for (int64_t t = 0; t < M * N; ++t) {                                                   \
+            C[t] = ZERO(sr);                                                                    \
+            argmax[t] = 0;                                                                      \
+        }                                                                                       \
+        if (M == 0 || N == 0 || K == 0) return 0;                                               \
+        T* pa = (T*)malloc(sizeof(T) * P_MC * P_KC);                                            \
+        T* pb = (T*)malloc(sizeof(T) * P_KC * P_NC);                                            \
+        if (!pa || !pb) {                                                                       \
+            free(pa);                                                                           \
+            free(pb);                                                                           \
+            return -2;                                                                          \
+        }                                                                                       \
+        const int64_t ldc = N;                                                                  \
+        for (int64_t jc = 0; jc < N; jc += P_NC) {                                              \
+            const int64_t nc = N - jc < P_NC ? N - jc : P_NC;                                   \
+            for (int64_t pc = 0; pc < K; pc += P_KC) {                                          \
+                const int64_t kc = K - pc < P_KC ? K - pc : P_KC;                               \
+                pack_b_##S(kc, nc, B + pc * N + jc, N, pb);                                     \
+                for (int64_t ic = 0; ic < M; ic += P_MC) {                                      \
+                    const int64_t mc = M - ic < P_MC ? M - ic : P_MC;                           \
+                    pack_a_##S(mc, kc, A + ic * K + pc, K, pa);                                 \
+                    for (int64_t jr = 0; jr * P_NR < nc; ++jr) {                                \
+                        const int64_t j0 = jr * P_NR;                                           \
+                        const int64_t nr = nc - j0 < P_NR ? nc - j0 : P_NR;                     \
+                        for (int64_t ir = 0; ir * P_MR < mc; ++ir) {                            \
+                            const int64_t i0 = ir * P_MR;                                       \
+                            const int64_t mr = mc - i0 < P_MR ? mc - i0 : P_MR;                 \
+                            micro_argmax_##S(sr, mr, nr, kc, pc, pa + ir * P_MR * kc,           \
+                                             pb + jr * P_NR * kc,                               \
+                                             C + (ic + i0) * ldc + (jc + j0),                   \
+                                             argmax + (ic + i0) * ldc + (jc + j0), ldc);        \
+                        }                                                                       \
+                    }                                                                           \
+                }                                                                               \
+            }                                                                                   \
+        }                                                                                       \
+        free(pa);                                                                               \
+        free(pb);                                                                               \
+        return 0;                                                                               \
+    }
+
+TGO_PORTABLE(float, f32, zero_f32, mul_f32)
+TGO_PORTABLE(int32_t, i32, zero_i32, mul_i32)
+
+/* ------------------------------------------------------------------------ */
+/* CPU BASELINE for value-only f32: the reference's AVX2 path                */
+/* (simd/kernels/avx2.rs: 8x8 f32 microkernels for MaxPlus, MinPlus and      */
+/*  MaxMul; core/gemm.rs:81-134 5-loop driver; tiling.rs F32_AVX2 = MC 256,  */
+/*  NC 256, KC 512, MR 8, NR 8; packing.rs:46-161 with MR = NR = 8).         */
+/* The microkernel keeps one 8-wide row of C per register, and per k         */
+/* broadcasts A[i,k] and combines it with the packed 8-wide row of B.        */
+/* ------------------------------------------------------------------------ */
+#include <immintrin.h>
+
+#define V_MC 256
+#define V_NC 256
+#define V_KC 512
+#define V_MR 8
+#define V_NR 8
+
+static void vpack_a_f32(int64_t mc, int64_t kc, const float* a, int64_t lda, float* packed) {
     int64_t p = 0;
-    for (int64_t r0 = 0; r0 < mc; r0 += P_MR)
+    for (int64_t r0 = 0; r0 < mc; r0 += V_MR)
         for (int64_t col = 0; col < kc; ++col)
-            for (int64_t ro = 0; ro < P_MR; ++ro) {
+            for (int64_t ro = 0; ro < V_MR; ++ro) {
                 const int64_t row = r0 + ro;
                 packed[p++] = row < mc ? a[row * lda + col] : 0.0f;
             }
 }
 
-/* pack_b: nr-column panels, k-major inside a panel, pad columns with 0. */
-static void pack_b_f32(int64_t kc, int64_t nc, const float* b, int64_t ldb, float* packed) {
+static void vpack_b_f32(int64_t kc, int64_t nc, const float* b, int64_t ldb, float* packed) {
     int64_t p = 0;
-    for (int64_t c0 = 0; c0 < nc; c0 += P_NR)
+    for (int64_t c0 = 0; c0 < nc; c0 += V_NR)
         for (int64_t row = 0; row < kc; ++row)
-            for (int64_t co = 0; co < P_NR; ++co) {
+            for (int64_t co = 0; co < V_NR; ++co) {
                 const int64_t col = c0 + co;
                 packed[p++] = col < nc ? b[row * ldb + col] : 0.0f;
             }
 }
 
-/* 4x4 microkernel with argmax: load (acc, idx) from C/argmax, visit
- * k = k_offset + p ascending with the CPU select rule, store back. */
-static void micro_argmax_f32(int sr, int64_t mr, int64_t nr, int64_t kc, int64_t k_offset,
-                             const float* pa, const float* pb, float* c, uint32_t* am,
-                             int64_t ldc) {
-    float acc[P_MR][P_NR];
-    uint32_t idx[P_MR][P_NR];
-    for (int64_t i = 0; i < P_MR; ++i)
-        for (int64_t j = 0; j < P_NR; ++j) {
-            acc[i][j] = zero_f32(sr);
-            idx[i][j] = 0;
+/* One 8x8 block: acc rows start as tropical zero, the valid mr x nr part is
+ * loaded from C; per k, acc[i] = acc[i] (+) (A[i,k] (x) B[k, 0..7]). */
+static void vmicro_f32(int sr, int64_t mr, int64_t nr, int64_t kc, const float* pa,
+                       const float* pb, float* c, int64_t ldc) {
+    __m256 acc[V_MR];
+    for (int64_t i = 0; i < V_MR; ++i) {
+        float row[V_NR];
+        for (int64_t j = 0; j < V_NR; ++j) row[j] = (i < mr && j < nr) ? c[i * ldc + j] : zero_f32(sr);
+        acc[i] = _mm256_loadu_ps(row);
+    }
+    if (sr == TGO_MAXPLUS) {
+        for (int64_t p = 0; p < kc; ++p) {
+            const __m256 bv = _mm256_loadu_ps(pb + p * V_NR);
+            for (int64_t i = 0; i < V_MR; ++i)
+                acc[i] = _mm256_max_ps(acc[i], _mm256_add_ps(_mm256_set1_ps(pa[p * V_MR + i]), bv));
         }
-    for (int64_t i = 0; i < mr; ++i)
-        for (int64_t j = 0; j < nr; ++j) {
-            acc[i][j] = c[i * ldc + j];
-            idx[i][j] = am[i * ldc + j];
+    } else if (sr == TGO_MINPLUS) {
+        for (int64_t p = 0; p < kc; ++p) {
+            const __m256 bv = _mm256_loadu_ps(pb + p * V_NR);
+            for (int64_t i = 0; i < V_MR; ++i)
+                acc[i] = _mm256_min_ps(acc[i], _mm256_add_ps(_mm256_set1_ps(pa[p * V_MR + i]), bv));
         }
-    for (int64_t p = 0; p < kc; ++p) {
-        const uint32_t cur = (uint32_t)(k_offset + p);
-        for (int64_t i = 0; i < mr; ++i) {
-            const float av = pa[p * P_MR + i];
-            for (int64_t j = 0; j < nr; ++j) {
-                const float prod = mul_f32(sr, av, pb[p * P_NR + j]);
-                const int keep = sr == TGO_MINPLUS ? (acc[i][j] <= prod) : (acc[i][j] >= prod);
-                if (!keep) {
-                    acc[i][j] = prod;
-                    idx[i][j] = cur;
-                }
-            }
+    } else {
+        for (int64_t p = 0; p < kc; ++p) {
+            const __m256 bv = _mm256_loadu_ps(pb + p * V_NR);
+            for (int64_t i = 0; i < V_MR; ++i)
+                acc[i] = _mm256_max_ps(acc[i], _mm256_mul_ps(_mm256_set1_ps(pa[p * V_MR + i]), bv));
         }
     }
-    for (int64_t i = 0; i < mr; ++i)
-        for (int64_t j = 0; j < nr; ++j) {
-            c[i * ldc + j] = acc[i][j];
-            am[i * ldc + j] = idx[i][j];
-        }
+    for (int64_t i = 0; i < mr; ++i) {
+        float row[V_NR];
+        _mm256_storeu_ps(row, acc[i]);
+        for (int64_t j = 0; j < nr; ++j) c[i * ldc + j] = row[j];
+    }
 }
 
-/* Row-major A (M x K), B (K x N); C/argmax are initialised here to tropical
- * zero / 0 exactly as GemmWithArgmax::new does (core/argmax.rs:24-33). */
-int tgo_portable_argmax_f32(int sr, const float* A, const float* B, float* C,
-                            uint32_t* argmax, int64_t M, int64_t N, int64_t K) {
+/* Row-major value-only C = A (x) B; C is initialised to tropical zero. */
+int tgo_avx2_gemm_f32(int sr, const float* A, const float* B, float* C, int64_t M, int64_t N,
+                      int64_t K) {
     if (sr < 0 || sr > 2 || M < 0 || N < 0 || K < 0) return -1;
-    for (int64_t t = 0; t < M * N; ++t) {
-        C[t] = zero_f32(sr);
-        argmax[t] = 0;
-    }
+    for (int64_t t = 0; t < M * N; ++t) C[t] = zero_f32(sr);
     if (M == 0 || N == 0 || K == 0) return 0;
-    float* pa = (float*)malloc(sizeof(float) * P_MC * P_KC);
-    float* pb = (float*)malloc(sizeof(float) * P_KC * P_NC);
-    const int64_t ldc = N;
-    for (int64_t jc = 0; jc < N; jc += P_NC) {
-        const int64_t nc = N - jc < P_NC ? N - jc : P_NC;
-        for (int64_t pc = 0; pc < K; pc += P_KC) {
-            const int64_t kc = K - pc < P_KC ? K - pc : P_KC;
-            pack_b_f32(kc, nc, B + pc * N + jc, N, pb);
-            for (int64_t ic = 0; ic < M; ic += P_MC) {
-                const int64_t mc = M - ic < P_MC ? M - ic : P_MC;
-                pack_a_f32(mc, kc, A + ic * K + pc, K, pa);
-                for (int64_t jr = 0; jr * P_NR < nc; ++jr) {
-                    const int64_t j0 = jr * P_NR;
-                    const int64_t nr = nc - j0 < P_NR ? nc - j0 : P_NR;
-                    for (int64_t ir = 0; ir * P_MR < mc; ++ir) {
-                        const int64_t i0 = ir * P_MR;
-                        const int64_t mr = mc - i0 < P_MR ? mc - i0 : P_MR;
-                        micro_argmax_f32(sr, mr, nr, kc, pc, pa + ir * P_MR * kc,
-                                         pb + jr * P_NR * kc, C + (ic + i0) * ldc + (jc + j0),
-                                         argmax + (ic + i0) * ldc + (jc + j0), ldc);
+    float* pa = (float*)malloc(sizeof(float) * V_MC * V_KC);
+    float* pb = (float*)malloc(sizeof(float) * V_KC * V_NC);
+    if (!pa || !pb) {
+        free(pa);
+        free(pb);
+        return -2;
+    }
+    for (int64_t jc = 0; jc < N; jc += V_NC) {
+        const int64_t nc = N - jc < V_NC ? N - jc : V_NC;
+        for (int64_t pc = 0; pc < K; pc += V_KC) {
+            const int64_t kc = K - pc < V_KC ? K - pc : V_KC;
+            vpack_b_f32(kc, nc, B + pc * N + jc, N, pb);
+            for (int64_t ic = 0; ic < M; ic += V_MC) {
+                const int64_t mc = M - ic < V_MC ? M - ic : V_MC;
+                vpack_a_f32(mc, kc, A + ic * K + pc, K, pa);
+                for (int64_t jr = 0; jr * V_NR < nc; ++jr) {
+                    const int64_t j0 = jr * V_NR;
+                    const int64_t nr = nc - j0 < V_NR ? nc - j0 : V_NR;
+                    for (int64_t ir = 0; ir * V_MR < mc; ++ir) {
+                        const int64_t i0 = ir * V_MR;
+                        const int64_t mr = mc - i0 < V_MR ? mc - i0 : V_MR;
+                        vmicro_f32(sr, mr, nr, kc, pa + ir * V_MR * kc, pb + jr * V_NR * kc,
+                                   C + (ic + i0) * N + (jc + j0), N);
                     }
                 }
             }
@@ -343,4 +469,4 @@ int tgo_portable_argmax_f32(int sr, const float* A, const float* B, float* C,
     return 0;
 }
 
-int tgo_version(void) { return 1; }
+int tgo_version(void) { return 2; }

@@ -1,6 +1,6 @@
 """bench.py keeps the driver's contract: one JSON line with the metric, the
-step timing, the roofline and (config P) the CPU baseline; more than one GPU
-is refused with a message."""
+step timing, the roofline and the CPU baseline; more than one GPU is refused
+with a message."""
 import json
 import os
 import subprocess
@@ -27,7 +27,7 @@ def test_more_than_one_gpu_is_refused():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("args", [("--config", "P", "--cpu-rows", "64"),
-                                  ("--config", "C1", "--cpu-rows", "0"),
+                                  ("--config", "C1"),
                                   ("--config", "M1"), ("--config", "E1")],
                          ids=["P", "C1", "M1", "E1"])
 def test_json_line(args):
@@ -49,7 +49,11 @@ def test_json_line(args):
     if args[1] == "M1":  # short K: HBM-bound, GB/s against 8 TB/s
         assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
         assert out["argmax_consistency_check"] is True
-    if args[1] == "P":
+    if args[1] in ("P", "C1", "M1"):
         base = out["cpu_baseline"]
         assert base["value"] > 0 and base["cores"] == 1 and base["kind"] in ("port", "reference")
+        assert "argmax" in base["sample"]
         assert out["argmax_consistency_check"] is True
+    if args[1] == "C1":  # the reference's value-only CPU path on the same product
+        base = out["cpu_baseline_value_only"]
+        assert base["value"] > 0 and base["cores"] == 1 and "AVX2" in base["sample"]

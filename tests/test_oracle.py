@@ -179,3 +179,37 @@ def test_portable_baseline_equals_oracle(sr):
     c2, a2 = oracle.portable_argmax_f32(sr, a, b)
     np.testing.assert_array_equal(tc.bits(c1), tc.bits(c2))
     np.testing.assert_array_equal(a1, a2)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_portable_baseline_i32_equals_oracle(sr):
+    # K = 300 crosses the 256-k block (the argmax carries k_offset); ties,
+    # and wrapping sums near the int32 limits.
+    rng = np.random.default_rng(12)
+    for lo, hi in ((-1000, 1001), (0, 3), (2**31 - 60, 2**31 - 1)):
+        a = rng.integers(lo, hi, size=(67, 300)).astype(np.int32)
+        b = rng.integers(-5, 60, size=(300, 130)).astype(np.int32)
+        c1, a1 = oracle.gemm(sr, a, b)
+        c2, a2 = oracle.portable_argmax(sr, a, b)
+        np.testing.assert_array_equal(c1, c2)
+        np.testing.assert_array_equal(a1, a2)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_avx2_value_baseline_equals_oracle(sr):
+    # 300 x 600 x 270 crosses every block edge of the 256/256/512 tiling and
+    # leaves partial 8 x 8 micro-blocks; MaxMul on positive data.
+    rng = np.random.default_rng(13)
+    if sr == "maxmul":
+        a = (1.0 - rng.random((300, 600))).astype(np.float32)
+        b = (1.0 - rng.random((600, 270))).astype(np.float32)
+    else:
+        a = rng.standard_normal((300, 600)).astype(np.float32)
+        b = rng.standard_normal((600, 270)).astype(np.float32)
+    c1, _ = oracle.gemm(sr, a, b, with_argmax=False)
+    c2 = oracle.avx2_gemm_f32(sr, a, b)
+    np.testing.assert_array_equal(tc.bits(c1), tc.bits(c2))
+    # Empty K: the tropical zero everywhere.
+    z = oracle.avx2_gemm_f32(sr, np.zeros((3, 0), np.float32), np.zeros((0, 5), np.float32))
+    np.testing.assert_array_equal(z, np.full((3, 5), {"maxplus": -np.inf, "minplus": np.inf,
+                                                      "maxmul": 0.0}[sr], np.float32))
