@@ -1,7 +1,8 @@
 """GPU backward (argmax scatter) and the PyTorch autograd mirror.
 
-Gradients are accumulated with atomics, so the order of the f32 sums is not
-fixed.  Tolerance, per element of grad_A / grad_B:
+Gradients are accumulated with LDS atomics (a compare-and-swap of the bits
+with a hardware-add fallback for f32, ds_add_f64 for f64), so the order of the
+sums is not fixed.  Tolerance, per element of grad_A / grad_B:
     |gpu - oracle| <= 4 * n_terms * 2^-24 * sum(|terms|)   (f32)
     |gpu - oracle| <= 4 * n_terms * 2^-53 * sum(|terms|)   (f64)
 where n_terms is how many upstream gradients land on that element; elements
@@ -71,6 +72,48 @@ def test_backward_matches_oracle(dtype, sr, shape):
     _tol_check(ga, ga_ref, s, cnt, eps)
     cnt, s = _contrib(am64, g, k, "b", a if mult else None)
     _tol_check(gb, gb_ref, s, cnt, eps)
+
+
+# Argmax patterns that steer the f32 LDS adds down each of their paths: one
+# compare-and-swap that wins (spread indices), CAS rounds that lose to other
+# lanes and fall back to the hardware add (paired or clustered indices), and
+# waves whose indices repeat so much that they take the hardware add outright.
+PATTERNS = ["uniform", "all zero", "four values", "k = j", "pairs", "row argmax"]
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("pattern", PATTERNS)
+def test_backward_index_patterns(dtype, pattern):
+    from tropical_gemm import ops
+
+    m, n, k = 192, 1024, 1024
+    rng = np.random.default_rng(23 + PATTERNS.index(pattern))
+    g = rng.standard_normal((m, n)).astype(dtype)
+    if pattern == "uniform":
+        am = rng.integers(0, k, size=(m, n))
+    elif pattern == "all zero":
+        am = np.zeros((m, n), np.int64)
+    elif pattern == "four values":
+        am = rng.integers(0, 4, size=(m, n))
+    elif pattern == "k = j":
+        am = np.tile(np.arange(n), (m, 1))
+    elif pattern == "pairs":  # lanes 2t and 2t+1 share an index
+        am = np.repeat(rng.integers(0, k, size=(m, n // 2)), 2, axis=1)
+    else:  # the argmax of N(0,1) data: a few hundred distinct k per row
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        _, am = oracle.gemm("maxplus", a, b)
+    am = am.astype(np.int64)
+    print(f"[case] backward pattern {pattern} {np.dtype(dtype).name}", flush=True)
+    tg = torch.from_numpy(g).to(DEV)
+    tam = torch.from_numpy(am.astype(np.int32)).to(DEV)
+    ga = ops.backward_a(tg, tam, k).cpu().numpy()
+    gb = ops.backward_b(tg, tam, k).cpu().numpy()
+    eps = 2.0**-24 if dtype == np.float32 else 2.0**-53
+    cnt, s = _contrib(am, g, k, "a")
+    _tol_check(ga, oracle.backward_a(g, am.astype(np.uint32), k), s, cnt, eps)
+    cnt, s = _contrib(am, g, k, "b")
+    _tol_check(gb, oracle.backward_b(g, am.astype(np.uint32), k), s, cnt, eps)
 
 
 def test_backward_column_major_and_out_of_range_index():
