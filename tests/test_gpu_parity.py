@@ -959,3 +959,52 @@ def test_exact_mode_strided_batches_and_misaligned_outputs(dt):
     torch.cuda.synchronize()
     assert_exact(c.cpu().numpy()[1:].reshape(m, n), am.cpu().numpy()[1:].reshape(m, n),
                  *oracle.gemm("minplus", a, b))
+
+
+# ---------------------------------------------------------------------------
+# Partial edge tiles in the direct-to-LDS kernels: M anything, N a multiple of
+# 4 (whole 16-byte groups), K a multiple of 32.  The loads of a partial tile
+# clamp into the matrix and the stores skip what lies outside it.
+# ---------------------------------------------------------------------------
+
+# The last three split K (few tiles, long K) with the full workspace and run
+# unsplit with the minimum one.
+PARTIAL_SHAPES = [(100, 64, 132, True), (65, 512, 68, True), (4100, 1024, 4100, True),
+                  (4100, 1024, 4096, True), (1, 416, 4, True), (130, 96, 260, False),
+                  (1, 32, 4, False), (4097, 640, 1028, False), (1000, 1024, 1000, True),
+                  (70, 2048, 68, True), (70, 2048, 68, False)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_direct_to_lds_partial_tiles(sr, dt):
+    rng = np.random.default_rng(400 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n, argmax) in PARTIAL_SHAPES:
+        print(f"[case] partial tiles {sr} {dt} m={m} k={k} n={n} argmax={argmax}", flush=True)
+        if sr == "maxmul" and dt == "f32":
+            a = (1.0 - rng.random((m, k))).astype(dtype)
+            b = (1.0 - rng.random((k, n))).astype(dtype)
+        else:
+            a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+            b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        ref = oracle.gemm(sr, a, b, with_argmax=argmax)
+        for api in ("alloc", "ws", "min"):
+            c, am = gpu_gemm(sr, a, b, argmax, api=api)
+            assert_exact(c, am, ref[0], ref[1] if argmax else None)
+
+
+def test_direct_to_lds_partial_tiles_batched_and_col_major():
+    """Strided batches with gaps and partial tiles; a column-major call whose
+    swapped operands make the kernel's M ragged."""
+    rng = np.random.default_rng(410)
+    items = [(rng.standard_normal((70, 256)).astype(np.float32),
+              rng.standard_normal((256, 132)).astype(np.float32)) for _ in range(3)]
+    print("[case] partial tiles batched", flush=True)
+    for (c, am), (a, b) in zip(_strided_batched("maxplus", items), items):
+        assert_exact(c, am, *oracle.gemm("maxplus", a, b))
+    a = rng.standard_normal((132, 512)).astype(np.float32)
+    b = rng.standard_normal((512, 70)).astype(np.float32)
+    print("[case] partial tiles column-major", flush=True)
+    c, am = gpu_gemm("minplus", a, b, True, layout="col")
+    assert_exact(c, am, *oracle.gemm("minplus", a, b))

@@ -196,13 +196,14 @@ WsLayout ws_layout(tg_dtype dt, int64_t batch, int64_t M, int64_t N, int64_t K, 
     return w;
 }
 
-// Direct-to-LDS kernel for 32-bit types when every tile is full.  splits > 1
-// runs K in that many slices into the workspace partials, then merges them.
+// Direct-to-LDS kernel for 32-bit types (partial edge tiles allowed, see
+// tg::dl_fits).  splits > 1 (full tiles only) runs K in that many slices into
+// the workspace partials, then merges them.
 template <int SR, typename T, int TN, int CL>
 int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     using Cfg = tg::DlCfg<TN>;
-    const int64_t tiles_m = p.M / Cfg::BM;
-    const int64_t tiles_n = p.N / Cfg::BN;
+    const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;  // the last ones may be partial
+    const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     if (tiles_m * tiles_n > 0x7fffffffLL)
         return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
     const T* A = static_cast<const T*>(p.A);
@@ -435,7 +436,11 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             pl.path = Path::KRES;
             return pl;
         }
-        if (!exact) {
+        // Partial tiles: argmax problems up to the generic kernel's exact
+        // limit stay there (no resolve); longer ones and value-only run the
+        // direct-to-LDS kernels with clamped loads.
+        const bool partial = !tg::dl_full_tiles<4>(p.M, p.N);
+        if (!exact && !(partial && argmax && p.K <= exact_tiles_max_k<T>())) {
             // Direct-to-LDS kernels (value-only, or argmax beyond the exact
             // range).  Split K when the problem makes too few 64 x 64 tiles
             // and the workspace holds the partials (tg_gemm_workspace_size
@@ -459,7 +464,9 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             // (value-only runs four workgroups per CU, small problems get
             // twice the tiles).
             const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
-                              (p.M / tg::DlCfg<8>::BM) * (p.N / tg::DlCfg<8>::BN) * p.batch >= 1536;
+                              ((p.M + tg::DlCfg<8>::BM - 1) / tg::DlCfg<8>::BM) *
+                                      (p.N / tg::DlCfg<8>::BN) * p.batch >=
+                                  1536;
             pl.splits = splits;
             if (wide && tg::dl_fits<8, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
                 pl.path = Path::DL_8_16;
@@ -628,15 +635,16 @@ size_t bt_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
 }
 
 // Full workspace: the minimum plus the split-K partials (values, and indices
-// for argmax) of 32-bit full-tile problems that make too few tiles
-// (tg::dl_splits, symmetric in m and n).  A workspace of at least the minimum
-// runs the same products unsplit.
+// for argmax) of 32-bit problems that make too few tiles (tg::dl_splits,
+// taken for both orientations: column-major calls swap m and n).  A
+// workspace of at least the minimum runs the same products unsplit.
 size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int64_t k,
                            bool with_argmax) {
     if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
     size_t w = bt_bytes_for(dt, batch, m, n, k, with_argmax);
     if (elem_size(dt) == 4) {
-        const int s = tg::dl_splits(m, n, k, batch);
+        const int s1 = tg::dl_splits(m, n, k, batch), s2 = tg::dl_splits(n, m, k, batch);
+        const int s = s1 > s2 ? s1 : s2;
         if (s > 1) {
             const size_t part = round_up(size_t(s) * size_t(batch) * size_t(m) * size_t(n) * 4, 256);
             w += part * (with_argmax ? 2 : 1);

@@ -85,25 +85,38 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// True when tg_gemm_dl<.., TN, CL> can run the problem: full tiles, 16-byte
-// aligned operands, outputs and batch strides (tiles load and store 16 bytes
-// per lane), and chunk indices that fit the epilogue's 16-bit slots.
+// True when tg_gemm_dl<.., TN, CL> can run the problem: K a multiple of the
+// 32-k tile, N a multiple of 4 and 16-byte aligned operands, outputs and
+// batch strides (tiles load and store 16 bytes per lane), and chunk indices
+// that fit the epilogue's 16-bit slots.  M and N need not fill the tiles:
+// the loads of a partial tile clamp their rows and columns into the matrix
+// (duplicates whose outputs are never stored), and the stores skip rows past
+// M and 4-column groups past N.
 template <int TN, int CL>
 inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC,
                     const void* A, const void* B, const void* C, const void* IDX) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     using Cfg = DlCfg<TN>;
-    return M > 0 && N > 0 && K > 0 && M % Cfg::BM == 0 && N % Cfg::BN == 0 &&
-           K % Cfg::BK == 0 && K / CL < 0xFFFF && sA % 4 == 0 && sB % 4 == 0 &&
-           sC % 4 == 0 && a16(A) && a16(B) && a16(C) && (IDX == nullptr || a16(IDX));
+    return M > 0 && N > 0 && K > 0 && N % 4 == 0 && K % Cfg::BK == 0 && K / CL < 0xFFFF &&
+           sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) &&
+           (IDX == nullptr || a16(IDX));
 }
 
-// Split K for full-tile problems with too few 64 x 64 tiles to fill the
-// chip: the largest power of two S with at most 1024 workgroups in total,
-// slices of at least 256 k and slice lengths that are multiples of 64.
+// True when every tile of the problem is full (the split-K and wide-tile
+// choices are made for those).
+template <int TN>
+inline bool dl_full_tiles(int64_t M, int64_t N) {
+    return M % DlCfg<TN>::BM == 0 && N % DlCfg<TN>::BN == 0;
+}
+
+// Split K for problems with too few 64 x 64 tiles (partial ones included) to
+// fill the chip: the largest power of two S with at most 1024 workgroups in
+// total, slices of at least 256 k and slice lengths that are multiples of 64.
+// N a multiple of 4, as the kernel needs (the merge then reads whole 16-byte
+// groups of the dense M x N partials).
 inline int dl_splits(int64_t M, int64_t N, int64_t K, int64_t batch) {
-    if (M % 64 != 0 || N % 64 != 0 || K % 64 != 0 || batch <= 0) return 1;
-    const int64_t tiles = (M / 64) * (N / 64) * batch;
+    if (M <= 0 || N <= 0 || N % 4 != 0 || K % 64 != 0 || batch <= 0) return 1;
+    const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64) * batch;
     int s = 1;
     while (tiles * s * 2 <= 1024 && K % (int64_t(64) * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
     return s;
@@ -114,7 +127,7 @@ inline int dl_splits(int64_t M, int64_t N, int64_t K, int64_t batch) {
 // better, so equal values keep the earlier slice's index and bits: the
 // reference's first-k rule across slices.  Partials are dense, slice stride
 // sY = batch * M * N; outputs use the batch stride sC.  16-byte vectors
-// (M * N is a multiple of 4096 here).
+// (N, so M * N, is a multiple of 4 here).
 template <int SR, typename T, bool ARGMAX>
 __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
                                                        const int32_t* __restrict__ PI,
@@ -188,20 +201,25 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
 
     // Per-lane global sources of this wave's direct loads (chunk 0).  A: 8
     // rows per 1 KB instruction, wave w issues instructions 2w, 2w+1.  B:
-    // RPI k-rows per instruction, wave w issues NBI*w .. NBI*w + NBI-1.
+    // RPI k-rows per instruction, wave w issues NBI*w .. NBI*w + NBI-1.  In a
+    // partial tile, rows past M read row M-1 and 4-column groups past N read
+    // the last group: in-bounds duplicates that only feed outputs that are
+    // never stored.
     const T* srcA[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int r = (wave * 2 + q) * 8 + (lane >> 3);
         const int qpos = lane & 7;
         const int qsrc = qpos ^ ((r >> 2) & 7);
-        srcA[q] = A + (row0 + r) * K + qsrc * 4;
+        const int64_t gr = row0 + r < M ? row0 + r : M - 1;
+        srcA[q] = A + gr * K + qsrc * 4;
     }
     const T* srcB[NBI];
 #pragma unroll
     for (int q = 0; q < NBI; ++q) {
         const int kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
-        srcB[q] = B + int64_t(kr) * N + col0 + (lane % Cfg::LPR) * 4;
+        const int64_t gc = col0 + (lane % Cfg::LPR) * 4;
+        srcB[q] = B + int64_t(kr) * N + (gc < N ? gc : N - 4);
     }
     auto issue_loads = [&](int64_t t, int buf) {
         T* adst = As0 + buf * (BM * BK);
@@ -297,9 +315,11 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     // tx*4 + (j&3); its local id is row*BN + column.
     auto store_row = [&](int i, const T (&v)[TN], const int32_t (&ix)[TN]) {
         const int64_t gr = row0 + ty * 4 + i;
+        if (gr >= M) return;
 #pragma unroll
         for (int g = 0; g < TN / 4; ++g) {
             const int64_t gc = col0 + g * 64 + tx * 4;
+            if (gc >= N) continue;  // N is a multiple of 4: whole groups only
             Vec16<T> cv;
 #pragma unroll
             for (int e = 0; e < 4; ++e) cv.v[e] = v[g * 4 + e];
@@ -405,8 +425,11 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 valid[g] = e < total;
                 lid[g] = valid[g] ? int(list[e]) : 0;
                 c[g] = valid[g] ? int64_t(chs[lid[g]]) : 0;
-                ap[g] = A + (row0 + lid[g] / BN) * K + c[g] * CL;
-                bp[g] = BT + (col0 + (lid[g] & (BN - 1))) * K + c[g] * CL;
+                // Clamped like the tile loads (outputs past M or N are not
+                // stored; their windows just stay in bounds).
+                const int64_t gr = row0 + lid[g] / BN, gc = col0 + (lid[g] & (BN - 1));
+                ap[g] = A + (gr < M ? gr : M - 1) * K + c[g] * CL;
+                bp[g] = BT + (gc < N ? gc : N - 1) * K + c[g] * CL;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
                     av[g][w] = reinterpret_cast<const Vec16<T>*>(ap[g])[w];
