@@ -62,9 +62,11 @@ KERNEL_NAMES = {
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md,
-# profiles/tg_gemm_tiles_exact_*.md).
-# Configs not profiled: None.
-TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9, "M1": 1.082e9}
+# profiles/tg_gemm_tiles_exact_*.md, profiles/hbm_traffic_c1_c2_c3_e1.md).  E1:
+# per GEMM launch.
+
+TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9, "M1": 1.082e9, "C1": 0.0742e9,
+           "C2": 1.775e9, "C3": 1.642e9, "E1": 0.1435e9}
 
 
 def cpu_model() -> str:
@@ -214,7 +216,7 @@ def run_einsum(args, lib, dev) -> int:
             "peak": PEAK_FP32_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC.get(args.config),  # per GEMM launch
             "kernel": "tg_gemm_dl<MaxPlus, f32, value-only> (every GEMM of the contraction)",
             "kernel_ms": round(ms_gemms, 4),
             "kernel_launches_timed": int(nl.value),
