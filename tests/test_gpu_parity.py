@@ -1008,3 +1008,39 @@ def test_direct_to_lds_partial_tiles_batched_and_col_major():
     print("[case] partial tiles column-major", flush=True)
     c, am = gpu_gemm("minplus", a, b, True, layout="col")
     assert_exact(c, am, *oracle.gemm("minplus", a, b))
+
+
+# K not a multiple of 32 (but of 4) in the direct-to-LDS kernels: the last
+# k-tile is partial and the last argmax chunk may end past K.  Argmax cases
+# have K above the exact mode's limit; "late" puts the maximum (and a tie) in
+# the last, partial chunk.
+RAGGED_K_SHAPES = [(130, 1000, 68, True), (65, 420, 132, True), (130, 100, 68, False),
+                   (1, 36, 4, False), (4100, 1000, 4100, True), (257, 644, 260, False)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_direct_to_lds_ragged_k(sr, dt):
+    rng = np.random.default_rng(420 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, k, n, argmax) in RAGGED_K_SHAPES:
+        for late in (False, True):
+            print(f"[case] ragged K {sr} {dt} m={m} k={k} n={n} argmax={argmax} late={late}",
+                  flush=True)
+            if sr == "maxmul" and dt == "f32":
+                a = (1.0 - rng.random((m, k))).astype(dtype)
+                b = (1.0 - rng.random((k, n))).astype(dtype)
+            else:
+                a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+                b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+            if late:
+                big = {"maxplus": 5000, "minplus": -5000, "maxmul": 5000}[sr]
+                a[:, k - 1] = big
+                a[:, k - 3] = big
+                b[k - 3] = np.abs(b[k - 3]) + 1  # at least 1: these products dominate
+                b[k - 1] = b[k - 3]  # the same product at k-3 and k-1: the first wins
+            ref = oracle.gemm(sr, a, b, with_argmax=argmax)
+            c, am = gpu_gemm(sr, a, b, argmax, api="ws")
+            assert_exact(c, am, ref[0], ref[1] if argmax else None)
+            if argmax and late and not (sr == "maxmul" and dt == "i32"):
+                assert np.all(am == k - 3)  # (i32 MaxMul: negative B can outweigh it)

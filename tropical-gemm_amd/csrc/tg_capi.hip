@@ -240,15 +240,36 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         int32_t* Iz = !argmax ? nullptr : splits > 1 ? PI + z0 * MN : p.IDX + z0 * p.sC;
         const int64_t sCk = splits > 1 ? MN : p.sC;
         dim3 grid(unsigned(tiles_m * tiles_n), unsigned(splits), unsigned(nb));
+        const bool tailk = p.K % Cfg::BK != 0;  // the last k-tile is partial
         if (argmax) {
             const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
-            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
-                               Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, sCk,
-                               int(tiles_m), int(tiles_n), KS, sY);
+            if (tailk) {
+                // 64 x 64 tiles only: the 64 x 128 kernel with the tail code
+                // would spill (the plan never picks it for a partial K).
+                if constexpr (TN == 4)
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL, true>), grid,
+                                       dim3(256), Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M,
+                                       p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS,
+                                       sY);
+                else
+                    return fail(TG_ERR_INVALID_ARGUMENT, "internal: 64x128 tiles need K % 32 == 0");
+            } else
+                hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL>), grid, dim3(256),
+                                   Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA,
+                                   p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
         } else {
-            hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL>), grid, dim3(256), Cfg::LDS_BYTES, st,
-                               Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K, p.sA, p.sB, sCk,
-                               int(tiles_m), int(tiles_n), KS, sY);
+            if (tailk) {
+                if constexpr (TN == 4)
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL, true>), grid,
+                                       dim3(256), Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz, nullptr,
+                                       p.M, p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n),
+                                       KS, sY);
+                else
+                    return fail(TG_ERR_INVALID_ARGUMENT, "internal: 64x128 tiles need K % 32 == 0");
+            } else
+                hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL>), grid, dim3(256),
+                                   Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K,
+                                   p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
         }
         TG_HIP(hipGetLastError());
     }
@@ -436,10 +457,10 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             pl.path = Path::KRES;
             return pl;
         }
-        // Partial tiles: argmax problems up to the generic kernel's exact
-        // limit stay there (no resolve); longer ones and value-only run the
-        // direct-to-LDS kernels with clamped loads.
-        const bool partial = !tg::dl_full_tiles<4>(p.M, p.N);
+        // Partial tiles (M, N or K): argmax problems up to the generic
+        // kernel's exact limit stay there (no resolve); longer ones and
+        // value-only run the direct-to-LDS kernels with clamped loads.
+        const bool partial = !tg::dl_full_tiles<4>(p.M, p.N, p.K);
         if (!exact && !(partial && argmax && p.K <= exact_tiles_max_k<T>())) {
             // Direct-to-LDS kernels (value-only, or argmax beyond the exact
             // range).  Split K when the problem makes too few 64 x 64 tiles
@@ -464,6 +485,7 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             // (value-only runs four workgroups per CU, small problems get
             // twice the tiles).
             const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
+                              p.K % tg::DlCfg<8>::BK == 0 &&
                               ((p.M + tg::DlCfg<8>::BM - 1) / tg::DlCfg<8>::BM) *
                                       (p.N / tg::DlCfg<8>::BN) * p.batch >=
                                   1536;

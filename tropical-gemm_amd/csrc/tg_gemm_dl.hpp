@@ -85,28 +85,27 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// True when tg_gemm_dl<.., TN, CL> can run the problem: K a multiple of the
-// 32-k tile, N a multiple of 4 and 16-byte aligned operands, outputs and
-// batch strides (tiles load and store 16 bytes per lane), and chunk indices
-// that fit the epilogue's 16-bit slots.  M and N need not fill the tiles:
-// the loads of a partial tile clamp their rows and columns into the matrix
-// (duplicates whose outputs are never stored), and the stores skip rows past
-// M and 4-column groups past N.
+// True when tg_gemm_dl<.., TN, CL> can run the problem: K and N multiples of
+// 4 and 16-byte aligned operands, outputs and batch strides (tiles load and
+// store 16 bytes per lane), and chunk indices that fit the epilogue's 16-bit
+// slots.  M, N and K need not fill the tiles: the loads of a partial tile
+// clamp their rows, columns and k into the matrix (in-bounds duplicates),
+// the k past K of the last k-tile are then overwritten in LDS with operands
+// whose product is the tropical zero, and the stores skip rows past M and
+// 4-column groups past N.
 template <int TN, int CL>
 inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC,
                     const void* A, const void* B, const void* C, const void* IDX) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    using Cfg = DlCfg<TN>;
-    return M > 0 && N > 0 && K > 0 && N % 4 == 0 && K % Cfg::BK == 0 && K / CL < 0xFFFF &&
+    return M > 0 && N > 0 && K > 0 && N % 4 == 0 && K % 4 == 0 && (K + CL - 1) / CL < 0xFFFF &&
            sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) &&
            (IDX == nullptr || a16(IDX));
 }
 
-// True when every tile of the problem is full (the split-K and wide-tile
-// choices are made for those).
+// True when every tile of the problem is full.
 template <int TN>
-inline bool dl_full_tiles(int64_t M, int64_t N) {
-    return M % DlCfg<TN>::BM == 0 && N % DlCfg<TN>::BN == 0;
+inline bool dl_full_tiles(int64_t M, int64_t N, int64_t K) {
+    return M % DlCfg<TN>::BM == 0 && N % DlCfg<TN>::BN == 0 && K % DlCfg<TN>::BK == 0;
 }
 
 // Split K for problems with too few 64 x 64 tiles (partial ones included) to
@@ -162,7 +161,9 @@ __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
 
 // Waves per SIMD come from the tile configuration (DlCfg): other resident
 // waves hide the LDS latency of the main loop.
-template <int SR, typename T, bool ARGMAX, int TN_, int CL>
+// TAILK: K is not a multiple of BK (the last k-tile is partial); a separate
+// instantiation, so full-K problems run the plain pipeline.
+template <int SR, typename T, bool ARGMAX, int TN_, int CL, bool TAILK = false>
 __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     ARGMAX ? DlCfg<TN_>::WAVES_ARGMAX : DlCfg<TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
@@ -231,6 +232,41 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         for (int q = 0; q < NBI; ++q)
             lds_load16(srcB[q] + t * BK * N, bdst + (wave * NBI + q) * 256);
     };
+    // The last k-tile when K is not a multiple of BK: A quads past K read the
+    // row's last quad and B rows past K read row K-1 (in bounds; overwritten
+    // in LDS by patch_tail before use).
+    auto issue_tail_loads = [&](int64_t t, int buf) {
+        T* adst = As0 + buf * (BM * BK);
+        T* bdst = Bs0 + buf * (BK * BN);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int r = (wave * 2 + q) * 8 + (lane >> 3);
+            const int qsrc = (lane & 7) ^ ((r >> 2) & 7);
+            const int64_t kq = t * BK + qsrc * 4;
+            lds_load16(srcA[q] - qsrc * 4 + (kq < K - 4 ? kq : K - 4), adst + (wave * 2 + q) * 256);
+        }
+#pragma unroll
+        for (int q = 0; q < NBI; ++q) {
+            const int kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
+            const int64_t kk = t * BK + kr;
+            lds_load16(srcB[q] - int64_t(kr) * N + (kk < K - 1 ? kk : K - 1) * N,
+                       bdst + (wave * NBI + q) * 256);
+        }
+    };
+    // k in [kv, BK) of the tile in buffer buf: A gets the tropical zero and B
+    // gets 0, so those products are the tropical zero (never an improvement;
+    // no infinities meet, and integers do not wrap).
+    auto patch_tail = [&](int buf, int kv) {
+        T* as = As0 + buf * (BM * BK);
+        T* bs = Bs0 + buf * (BK * BN);
+        const int na = BM * (BK - kv);
+        for (int e = tid; e < na; e += TG_THREADS) {
+            const int r = e / (BK - kv), k = kv + e % (BK - kv);
+            as[r * BK + (((k >> 2) ^ ((r >> 2) & 7)) << 2) + (k & 3)] = tzero<SR, T>();
+        }
+        const int nb = (BK - kv) * BN;
+        for (int e = tid; e < nb; e += TG_THREADS) bs[kv * BN + e] = T(0);
+    };
 
     T acc[TM][TN];
     int32_t ch[TM][TN];
@@ -262,14 +298,29 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     };
 
     // k-tiles [t0, t1) of this slice; t (and so every chunk index) is global.
+    // Split slices are whole k-tiles; an unsplit K may end in a partial one
+    // holding kv valid k.
     const int64_t t0 = y * (KS / BK);
-    const int64_t t1 = t0 + KS / BK;
-    issue_loads(t0, 0);
+    const int64_t t1 = t0 + (KS + BK - 1) / BK;
+    const int kv = TAILK ? int(KS - (t1 - 1 - t0) * BK) : BK;
+    if (TAILK && t1 - 1 == t0)
+        issue_tail_loads(t0, 0);
+    else
+        issue_loads(t0, 0);
     for (int64_t t = t0; t < t1; ++t) {
         const int buf = int((t - t0) & 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (t + 1 < t1) issue_loads(t + 1, buf ^ 1);
+        if (t + 1 < t1) {
+            if (TAILK && t + 2 == t1)
+                issue_tail_loads(t + 1, buf ^ 1);
+            else
+                issue_loads(t + 1, buf ^ 1);
+        }
+        if (TAILK && t + 1 == t1) {
+            patch_tail(buf, kv);
+            __syncthreads();
+        }
 
         // The LDS tile holds BK / CL argmax chunks of CL consecutive k.  Each
         // chunk folds its products into a max3/min3 chain that starts from
@@ -355,7 +406,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         uint8_t* res = dl_lds + Cfg::RES_OFF;
         int* misc = reinterpret_cast<int*>(dl_lds + Cfg::MISC_OFF);
         // Buckets: chunk >> shift, at most NB_MAX of them.
-        const int64_t nchunks = K / CL;
+        const int64_t nchunks = (K + CL - 1) / CL;
         int shift = 0;
         while (((nchunks - 1) >> shift) >= Cfg::NB_MAX) ++shift;
         const int nb = int(((nchunks - 1) >> shift) + 1);
@@ -426,14 +477,18 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 lid[g] = valid[g] ? int(list[e]) : 0;
                 c[g] = valid[g] ? int64_t(chs[lid[g]]) : 0;
                 // Clamped like the tile loads (outputs past M or N are not
-                // stored; their windows just stay in bounds).
+                // stored; their windows just stay in bounds).  Quads of a
+                // window past K read the row's last quad: duplicates that
+                // come after their originals, so the first match is a k < K.
                 const int64_t gr = row0 + lid[g] / BN, gc = col0 + (lid[g] & (BN - 1));
                 ap[g] = A + (gr < M ? gr : M - 1) * K + c[g] * CL;
                 bp[g] = BT + (gc < N ? gc : N - 1) * K + c[g] * CL;
 #pragma unroll
                 for (int w = 0; w < NW; ++w) {
-                    av[g][w] = reinterpret_cast<const Vec16<T>*>(ap[g])[w];
-                    bv[g][w] = reinterpret_cast<const Vec16<T>*>(bp[g])[w];
+                    const int64_t off =
+                        (!TAILK || c[g] * CL + w * 4 <= K - 4) ? w * 4 : K - 4 - c[g] * CL;
+                    av[g][w] = *reinterpret_cast<const Vec16<T>*>(ap[g] + off);
+                    bv[g][w] = *reinterpret_cast<const Vec16<T>*>(bp[g] + off);
                 }
             }
 #pragma unroll
