@@ -65,7 +65,7 @@ KERNEL_NAMES = {
 # profiles/tg_gemm_tiles_exact_*.md, profiles/hbm_traffic_c1_c2_c3_e1.md).  E1:
 # per GEMM launch.
 
-TRAFFIC = {"P": 1.938e9, "C5": 1.938e9, "C4": 0.403e9, "M1": 1.082e9, "C1": 0.0742e9,
+TRAFFIC = {"P": 1.929e9, "C5": 1.929e9, "C4": 0.403e9, "M1": 1.082e9, "C1": 0.0742e9,
            "C2": 1.775e9, "C3": 1.642e9, "E1": 0.1435e9}
 
 
