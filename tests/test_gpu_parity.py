@@ -1008,6 +1008,14 @@ def test_direct_to_lds_partial_tiles_batched_and_col_major():
     print("[case] partial tiles column-major", flush=True)
     c, am = gpu_gemm("minplus", a, b, True, layout="col")
     assert_exact(c, am, *oracle.gemm("minplus", a, b))
+    # Column-major split K: the kernel's N is m (68), its M is n (70); the
+    # workspace size covers both orientations.
+    a = rng.standard_normal((68, 2048)).astype(np.float32)
+    b = rng.standard_normal((2048, 70)).astype(np.float32)
+    ref = oracle.gemm("maxplus", a, b)
+    for api in ("alloc", "ws", "min"):
+        print(f"[case] partial tiles column-major split K api={api}", flush=True)
+        assert_exact(*gpu_gemm("maxplus", a, b, True, layout="col", api=api), *ref)
 
 
 # K not a multiple of 32 (but of 4) in the direct-to-LDS kernels: the last
