@@ -466,7 +466,11 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
         // kernel's exact mode (no resolve); longer ones and value-only run
         // the direct-to-LDS kernels with clamped loads.
         const bool partial = !tg::dl_full_tiles<4>(p.M, p.N, p.K);
-        if (!exact && !(partial && argmax && p.K <= kExactPartialMaxK)) {
+        // Value-only with K below 64 and not a multiple of 32: most of the
+        // direct-to-LDS kernel's padded last k-tile would be wasted work;
+        // the generic kernel bounds its last tile instead.
+        const bool short_tail = !argmax && p.K % 32 != 0 && p.K < 64;
+        if (!exact && !short_tail && !(partial && argmax && p.K <= kExactPartialMaxK)) {
             // Direct-to-LDS kernels (value-only, or argmax beyond the exact
             // range).  Split K when the problem makes too few 64 x 64 tiles
             // and the workspace holds the partials (tg_gemm_workspace_size
