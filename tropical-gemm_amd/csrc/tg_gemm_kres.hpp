@@ -244,10 +244,18 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 
         T* Ct = C + z * sC + tm * BM * N;
         int32_t* It = IDX + z * sC + tm * BM * N;
+        // Outputs are written once and not read back by this kernel: non-temporal
+        // 16-byte stores keep them from displacing the A/B panels in L2.
+        typedef int v4i_t __attribute__((ext_vector_type(4)));
+        auto stream16 = [](void* p, const void* v) {
+            v4i_t x;
+            __builtin_memcpy(&x, v, 16);
+            __builtin_nontemporal_store(x, reinterpret_cast<v4i_t*>(p));
+        };
         auto store_row = [&](int i, const Vec16<T>& cv, const Vec16<int32_t>& iv) {
             const int64_t off = int64_t(ty * 4 + i) * N + col0 + tx * 4;
-            *reinterpret_cast<Vec16<T>*>(Ct + off) = cv;
-            *reinterpret_cast<Vec16<int32_t>*>(It + off) = iv;
+            stream16(Ct + off, &cv);
+            stream16(It + off, &iv);
         };
 
         if constexpr (KEYS) {
