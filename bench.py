@@ -35,10 +35,12 @@ sys.path.insert(0, os.path.join(ROOT, "tropical-gemm_amd"))
 METRIC = ("tropical GOP/s (2·M·N·K) MaxPlus f32 4096³ +argmax, 1 GPU; "
           "% VALU peak")
 PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector (and dense) peak
-# Tropical roofline: (x) and (+) are one VALU op each with no fused form; the
-# densest mix (v_add_f32 + half a v_max3_f32) issues 2 tropical ops per 4
-# wave64-cycles per lane, i.e. half the FMA peak: 78.6e12 ops/s at 2.4 GHz.
-TROP_PEAK_TOPS = PEAK_FP32_TFLOPS / 2
+# Tropical roofline: (x) and (+) have no fused form. The densest exact mix is
+# one v_add_f32 per product plus half a v_max3_f32 (2 tropical ops per 1.5 VALU
+# instructions), and v_max3_f32 issues at the same rate as v_add_f32 and
+# v_fma_f32. At the FP32 instruction peak (157.3 TFLOP/s = 78.6e12 FMA
+# lane-instructions/s) that is 157.3 * 2/3 = 104.9e12 tropical ops/s.
+TROP_PEAK_TOPS = PEAK_FP32_TFLOPS * 2 / 3
 PEAK_HBM_GBS = 8000.0         # MI355X published HBM3E bandwidth
 DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
 WORKLOAD_NAMES = {
