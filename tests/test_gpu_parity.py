@@ -1052,3 +1052,60 @@ def test_direct_to_lds_ragged_k(sr, dt):
             assert_exact(c, am, ref[0], ref[1] if argmax else None)
             if argmax and late and not (sr == "maxmul" and dt == "i32"):
                 assert np.all(am == k - 3)  # (i32 MaxMul: negative B can outweigh it)
+
+
+# The short-K kernel (32-bit types, N % 4 == 0, K up to 32 with argmax and
+# up to 63 value-only): 32 x 256 tiles, 8 rows per wave read through scalar
+# loads in blocks of 8 k.  Rows past M inside a wave, column quads past N,
+# K around the 8-k blocks, wrapping i32 products, and strided batches whose
+# A rows start at odd element offsets.
+SHORT_K_SHAPES = [(1, 4, 1), (5, 260, 7), (33, 252, 8), (70, 516, 9), (8, 1028, 17),
+                  (100, 64, 24), (41, 300, 32)]
+
+
+@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_short_k_kernel_edges(sr, dt):
+    rng = np.random.default_rng(330 + tc.SEMIRINGS.index(sr))
+    dtype = tc.NP_DTYPES[dt]
+    for (m, n, k) in SHORT_K_SHAPES + [(37, 132, 40), (9, 260, 63)]:
+        print(f"[case] short-k {sr} {dt} m={m} n={n} k={k}", flush=True)
+        a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+        b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+        ref = oracle.gemm(sr, a, b)
+        c, _ = gpu_gemm(sr, a, b, False)
+        assert_exact(c, None, ref[0], None)
+        if k <= 32:
+            assert_exact(*gpu_gemm(sr, a, b, True), *ref)
+
+
+def test_short_k_kernel_integer_wrap_and_ties():
+    """i32 products that wrap (MaxPlus adds near the type's limits, MaxMul
+    products past 2^31) and all-equal products (argmax 0 everywhere)."""
+    rng = np.random.default_rng(340)
+    m, n, k = 45, 132, 12
+    big = np.iinfo(np.int32).max
+    a = rng.integers(big - 1000, big, size=(m, k), dtype=np.int64).astype(np.int32)
+    b = rng.integers(0, 2000, size=(k, n)).astype(np.int32)
+    for sr in ("maxplus", "minplus"):
+        assert_exact(*gpu_gemm(sr, a, b), *oracle.gemm(sr, a, b))
+    a = rng.integers(40000, 60000, size=(m, k)).astype(np.int32)
+    b = rng.integers(40000, 60000, size=(k, n)).astype(np.int32)
+    assert_exact(*gpu_gemm("maxmul", a, b), *oracle.gemm("maxmul", a, b))
+    a = np.full((m, k), 3, np.float32)
+    b = np.full((k, n), -1, np.float32)
+    c, am = gpu_gemm("maxplus", a, b)
+    assert np.all(c == 2) and np.all(am == 0)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_short_k_kernel_strided_batches(sr):
+    rng = np.random.default_rng(350 + tc.SEMIRINGS.index(sr))
+    m, k, n = 43, 9, 264
+    items = [(tc.rng_matrix(rng, np.float32, (m, k), -100, 100),
+              tc.rng_matrix(rng, np.float32, (k, n), -100, 100)) for _ in range(3)]
+    for gap_a in (3, 1):
+        print(f"[case] short-k strided {sr} gap_a={gap_a}", flush=True)
+        out = _strided_batched(sr, items, gap_a=gap_a, gap_c=4)
+        for (x, y), (c, am) in zip(items, out):
+            assert_exact(c, am, *oracle.gemm(sr, x, y))
