@@ -59,15 +59,15 @@ KERNEL_NAMES = {
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
     "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
-    "M1": "tg_gemm_tiles<MaxPlus, f32, argmax, exact> (128x64 tiles, per-product index)",
+    "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md,
-# profiles/tg_gemm_tiles_exact_*.md, profiles/hbm_traffic_c1_c2_c3_e1.md).  E1:
+# profiles/tg_gemm_shortk_*.md, profiles/hbm_traffic_c1_c2_c3_e1.md).  E1:
 # per GEMM launch.
 
-TRAFFIC = {"P": 1.929e9, "C5": 1.929e9, "C4": 0.403e9, "M1": 1.082e9, "C1": 0.0742e9,
+TRAFFIC = {"P": 1.929e9, "C5": 1.929e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.0742e9,
            "C2": 1.775e9, "C3": 1.642e9, "E1": 0.1435e9}
 
 
