@@ -1054,16 +1054,16 @@ def test_direct_to_lds_ragged_k(sr, dt):
                 assert np.all(am == k - 3)  # (i32 MaxMul: negative B can outweigh it)
 
 
-# The short-K kernel (32-bit types, N % 4 == 0, K up to 32 with argmax and
-# up to 63 value-only): 32 x 256 tiles, 8 rows per wave read through scalar
-# loads in blocks of 8 k.  Rows past M inside a wave, column quads past N,
+# The short-K kernel (N % 4 == 0, K up to 32 with argmax and up to 63
+# value-only): 32 x 256 tiles with 8 rows per wave for 32-bit types, 16 x 256
+# with 4 rows for 64-bit ones, A read through scalar loads in 32-byte blocks.  Rows past M inside a wave, column quads past N,
 # K around the 8-k blocks, wrapping i32 products, and strided batches whose
 # A rows start at odd element offsets.
 SHORT_K_SHAPES = [(1, 4, 1), (5, 260, 7), (33, 252, 8), (70, 516, 9), (8, 1028, 17),
                   (100, 64, 24), (41, 300, 32)]
 
 
-@pytest.mark.parametrize("dt", ["f32", "i32"])
+@pytest.mark.parametrize("dt", ["f32", "f64", "i32", "i64"])
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
 def test_short_k_kernel_edges(sr, dt):
     rng = np.random.default_rng(330 + tc.SEMIRINGS.index(sr))

@@ -385,10 +385,11 @@ int run_gemm_kres8(const Problem& p, hipStream_t st) {
     return TG_OK;
 }
 
-// Short-K kernel (32-bit types): 32 x 256 tiles written as 1 KB row runs.
+// Short-K kernel: 32 x 256 (64-bit types: 16 x 256) tiles written as 1 KB
+// row runs.
 template <int SR, typename T>
 int run_gemm_shortk(const Problem& p, hipStream_t st) {
-    using Cfg = tg::ShortkCfg;
+    using Cfg = tg::ShortkCfg<T>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
     const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     if (tiles_m * tiles_n > 0x7fffffffLL)
@@ -452,12 +453,14 @@ constexpr int64_t exact_tiles_max_k() {
     return sizeof(T) == 4 ? 384 : std::is_same<T, int64_t>::value ? 2048 : 512;
 }
 
-// 32-bit problems with K up to these run the short-K kernel (when N % 4 == 0
-// and B, C, IDX are 16-byte aligned).  Measured on MI355X (f32 MaxPlus,
-// 65536 x 2048 x K, against the kernels these problems took before): argmax
-// K = 8 183 us against 251 (generic tiles, exact mode), K = 32 403 against
-// 417, K = 48 567 against 554; value-only K = 8 104 against 143, K = 48 253
-// against 336, K = 64 344 against 343 (direct-to-LDS).
+// Problems with K up to these run the short-K kernel (when N % 4 == 0 and B,
+// C, IDX are 16-byte aligned).  Measured on MI355X (MaxPlus, against the
+// kernels these problems took before): f32 65536 x 2048 x K, argmax K = 8
+// 183 us against 251 (generic tiles, exact mode), K = 32 403 against 417,
+// K = 48 567 against 554; value-only K = 8 104 against 143, K = 48 253
+// against 336, K = 64 344 against 343 (direct-to-LDS); f64 8192^2 x K,
+// argmax K = 8 163 against 236, K = 32 335 against 390; value-only K = 63
+// 368 against 434.
 constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
@@ -490,12 +493,12 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
     Plan pl;
     const bool argmax = p.IDX != nullptr;
     const bool exact = argmax && p.K <= kExactMaxK;
+    if (p.K <= (argmax ? kShortkArgmaxMaxK : kShortkValueMaxK) &&
+        tg::shortk_fits(p.M, p.N, p.K, p.sB, p.sC, p.B, p.C, p.IDX)) {
+        pl.path = Path::SHORTK;
+        return pl;
+    }
     if constexpr (sizeof(T) == 4) {
-        if (p.K <= (argmax ? kShortkArgmaxMaxK : kShortkValueMaxK) &&
-            tg::shortk_fits(p.M, p.N, p.K, p.sB, p.sC, p.B, p.C, p.IDX)) {
-            pl.path = Path::SHORTK;
-            return pl;
-        }
         if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL) {
             if (argmax && tg::kres8_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
                 pl.path = Path::KRES8;
@@ -575,9 +578,9 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
 template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
     const Plan pl = plan_typed<SR, T>(p, ws_bytes);
+    if (pl.path == Path::SHORTK) return run_gemm_shortk<SR, T>(p, st);
     if constexpr (sizeof(T) == 4) {
         switch (pl.path) {
-            case Path::SHORTK: return run_gemm_shortk<SR, T>(p, st);
             case Path::KRES8:
                 if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL)
                     return run_gemm_kres8<SR>(p, st);

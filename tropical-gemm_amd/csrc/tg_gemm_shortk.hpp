@@ -1,28 +1,29 @@
-// tg_gemm_shortk.hpp -- tropical GEMM for short K, 32-bit types (gfx950).
+// tg_gemm_shortk.hpp -- tropical GEMM for short K (gfx950).
 //
 // At short K the product costs a few VALU ops per output against 4 (value) +
 // 4 (argmax) bytes written per output, so the kernel is shaped for the
 // writes rather than for operand reuse:
-//   * 32 x 256 output tiles taken in row-major tile order; wave w of the
-//     256-thread workgroup owns tile rows 8w .. 8w+7 and lane l owns columns
-//     4l .. 4l+3, so each store instruction of a wave writes 1 KB of one row.
+//   * 32 x 256 output tiles (16 x 256 for 64-bit types) taken in row-major
+//     tile order; wave w of the 256-thread workgroup owns tile rows
+//     R*w .. R*w+R-1 (R = 8, or 4 for 64-bit types) and lane l owns columns
+//     4l .. 4l+3, so the wave's stores cover 1 KB (2 KB) runs of one row.
 //     (A store probe on MI355X writing 2 x 512 MB: 1 KB row runs reach the
 //     hipMemset rate, 6.5 TB/s; the 256 B runs of 128 x 64 tiles 5.8 TB/s.)
-//   * A is wave-uniform: a wave reads its 8 rows' k values with scalar loads
-//     and the VALU takes them as SGPR operands.
+//   * A is wave-uniform: a wave reads its R rows' k values with scalar loads
+//     (32 bytes per row and block) and the VALU takes them as SGPR operands.
 //   * B rows are 16-byte vector loads, 1 KB per wave and k, served from L1/L2
 //     (B is K x N, small at short K, and re-read by every wave).
-//   * No LDS and about 100 VGPRs, so 4+ waves per SIMD keep the products of
-//     some waves in flight while others store.
+//   * No LDS and at most 128 VGPRs (f32 argmax: 124), so 4 waves per SIMD
+//     keep the products of some waves in flight while others store.
 // ARGMAX: every product in k order updates (value, k) on a strict
 // improvement, which keeps the first k attaining the optimum (the
 // reference's tie rule, core/argmax.rs:24-33 and core/kernel.rs:119-167);
 // outputs that never beat the tropical zero keep it with argmax 0.
 // Value-only: max3/min3 chains from the tropical zero.
 //
-// Host-checked requirements: 32-bit T, N % 4 == 0, B, C (and IDX) 16-byte
-// aligned with batch strides sB, sC multiples of 4; any M >= 1, K >= 1.
-// grid = (ceil(M / 32) * ceil(N / 256), 1, batch), block = 256.
+// Host-checked requirements: N % 4 == 0, B, C (and IDX) 16-byte aligned with
+// batch strides sB, sC multiples of 4; any M >= 1, K >= 1.
+// grid = (ceil(M / BM) * ceil(N / 256), 1, batch), block = 256.
 #pragma once
 
 #include <type_traits>
@@ -32,10 +33,11 @@
 
 namespace tg {
 
+template <typename T>
 struct ShortkCfg {
-    static constexpr int BM = 32, BN = 256;
-    static constexpr int R = 8;   // rows per wave
-    static constexpr int KB = 8;  // k per scalar-load block
+    static constexpr int R = sizeof(T) == 4 ? 8 : 4;  // rows per wave
+    static constexpr int KB = 32 / int(sizeof(T));    // k per scalar-load block
+    static constexpr int BM = 4 * R, BN = 256;
 };
 
 template <int SR, typename T, bool ARGMAX>
@@ -43,8 +45,9 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
     const T* __restrict__ A, const T* __restrict__ B, T* __restrict__ C,
     int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB,
     int64_t sC, int tiles_n) {
-    static_assert(sizeof(T) == 4, "short-K kernel is for 32-bit types");
-    constexpr int R = ShortkCfg::R, KB = ShortkCfg::KB;
+    using Cfg = ShortkCfg<T>;
+    constexpr int R = Cfg::R, KB = Cfg::KB;
+    constexpr int VN = Vec16<T>::N;  // elements per 16-byte vector
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
     const int tm = int(blockIdx.x) / tiles_n;
@@ -55,8 +58,8 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
     C += z * sC;
     if constexpr (ARGMAX) IDX += z * sC;
 
-    const int64_t r0 = int64_t(tm) * ShortkCfg::BM + w * R;
-    const int64_t col = int64_t(tn) * ShortkCfg::BN + lane * 4;
+    const int64_t r0 = int64_t(tm) * Cfg::BM + w * R;
+    const int64_t col = int64_t(tn) * Cfg::BN + lane * 4;
     const bool col_ok = col < N;
     const int64_t colc = col_ok ? col : N - 4;  // in-range column quad for loads
     // Row pointers, wave-uniform; rows past M read row M-1 and store nothing.
@@ -79,14 +82,20 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
     auto block = [&](int64_t k0, auto nk) {
         constexpr int NK = decltype(nk)::value;
         T a[R][NK];
-        Vec16<T> b[NK];
+        T b[NK][4];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int kk = 0; kk < NK; ++kk) a[r][kk] = arow[r][k0 + kk];
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk)
-            b[kk] = *reinterpret_cast<const Vec16<T>*>(B + (k0 + kk) * N + colc);
+#pragma unroll
+            for (int h = 0; h < 4 / VN; ++h) {
+                const Vec16<T> v =
+                    *reinterpret_cast<const Vec16<T>*>(B + (k0 + kk) * N + colc + h * VN);
+#pragma unroll
+                for (int e = 0; e < VN; ++e) b[kk][h * VN + e] = v.v[e];
+            }
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) {
             const int32_t kg = int32_t(k0 + kk);
@@ -94,7 +103,7 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
             for (int r = 0; r < R; ++r)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const T p = tmul<SR, T>(a[r][kk], b[kk].v[j]);
+                    const T p = tmul<SR, T>(a[r][kk], b[kk][j]);
                     if constexpr (ARGMAX) {
                         const bool better = tbetter<SR, T>(p, acc[r][j]);
                         acc[r][j] = better ? p : acc[r][j];
@@ -114,7 +123,9 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
     for (int r = 0; r < R; ++r) {
         if (r0 + r >= M) break;
         const int64_t off = (r0 + r) * N + col;
-        *reinterpret_cast<Vec16<T>*>(C + off) = *reinterpret_cast<const Vec16<T>*>(acc[r]);
+#pragma unroll
+        for (int h = 0; h < 4 / VN; ++h)
+            reinterpret_cast<Vec16<T>*>(C + off)[h] = reinterpret_cast<const Vec16<T>*>(acc[r])[h];
         if constexpr (ARGMAX)
             *reinterpret_cast<Vec16<int32_t>*>(IDX + off) =
                 *reinterpret_cast<const Vec16<int32_t>*>(ix[r]);
