@@ -100,18 +100,26 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
         for (int kk = 0; kk < NK; ++kk) {
             const int32_t kg = int32_t(k0 + kk);
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r) {
+                // The four compares of a row come before their selects, so no
+                // select waits on the compare just issued (no hazard s_nop).
+                T p[4];
+                bool better[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const T p = tmul<SR, T>(a[r][kk], b[kk][j]);
-                    if constexpr (ARGMAX) {
-                        const bool better = tbetter<SR, T>(p, acc[r][j]);
-                        acc[r][j] = better ? p : acc[r][j];
-                        ix[r][j] = better ? kg : ix[r][j];
-                    } else {
-                        acc[r][j] = tjoin<SR, T>(acc[r][j], p);
+                for (int j = 0; j < 4; ++j) p[j] = tmul<SR, T>(a[r][kk], b[kk][j]);
+                if constexpr (ARGMAX) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) better[j] = tbetter<SR, T>(p[j], acc[r][j]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[r][j] = better[j] ? p[j] : acc[r][j];
+                        ix[r][j] = better[j] ? kg : ix[r][j];
                     }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[r][j] = tjoin<SR, T>(acc[r][j], p[j]);
                 }
+            }
         }
     };
     int64_t k0 = 0;
