@@ -243,15 +243,38 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                 T a0[TM], b0[TN];
                 load_frag(buf, kk, a0, b0);
                 const int32_t kg = int32_t(k0 + kk);
+                if constexpr (sizeof(T) == 8) {
+                    // A row's compares come before their selects, so no
+                    // select waits on the compare just issued (no hazard
+                    // s_nop): 7% faster for 64-bit types.  For 32-bit types
+                    // the grouping needs 175 VGPRs instead of 155 (2 waves per
+                    // SIMD instead of 3) and was 9-15% slower.
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                    for (int i = 0; i < TM; ++i) {
+                        T p[TN];
+                        bool better[TN];
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        const T p = tmul<SR, T>(a0[i], b0[j]);
-                        const bool better = tbetter<SR, T>(p, acc[i][j]);
-                        acc[i][j] = better ? p : acc[i][j];
-                        ch[i][j] = better ? kg : ch[i][j];
+                        for (int j = 0; j < TN; ++j) {
+                            p[j] = tmul<SR, T>(a0[i], b0[j]);
+                            better[j] = tbetter<SR, T>(p[j], acc[i][j]);
+                        }
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            acc[i][j] = better[j] ? p[j] : acc[i][j];
+                            ch[i][j] = better[j] ? kg : ch[i][j];
+                        }
                     }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            const T p = tmul<SR, T>(a0[i], b0[j]);
+                            const bool better = tbetter<SR, T>(p, acc[i][j]);
+                            acc[i][j] = better ? p : acc[i][j];
+                            ch[i][j] = better ? kg : ch[i][j];
+                        }
+                }
             };
             const int kcnt = k0 + BK <= K ? BK : int(K - k0);
 #pragma unroll 4
