@@ -1059,7 +1059,7 @@ def test_direct_to_lds_ragged_k(sr, dt):
 # with 4 rows for 64-bit ones, A read through scalar loads in 32-byte blocks.  Rows past M inside a wave, column quads past N,
 # K around the 8-k blocks, wrapping i32 products, and strided batches whose
 # A rows start at odd element offsets.
-SHORT_K_SHAPES = [(1, 4, 1), (5, 260, 7), (33, 252, 8), (70, 516, 9), (8, 1028, 17),
+SHORTK_KERNEL_SHAPES = [(1, 4, 1), (5, 260, 7), (33, 252, 8), (70, 516, 9), (8, 1028, 17),
                   (100, 64, 24), (41, 300, 32)]
 
 
@@ -1068,7 +1068,7 @@ SHORT_K_SHAPES = [(1, 4, 1), (5, 260, 7), (33, 252, 8), (70, 516, 9), (8, 1028, 
 def test_short_k_kernel_edges(sr, dt):
     rng = np.random.default_rng(330 + tc.SEMIRINGS.index(sr))
     dtype = tc.NP_DTYPES[dt]
-    for (m, n, k) in SHORT_K_SHAPES + [(37, 132, 40), (9, 260, 63)]:
+    for (m, n, k) in SHORTK_KERNEL_SHAPES + [(37, 132, 40), (9, 260, 63)]:
         print(f"[case] short-k {sr} {dt} m={m} n={n} k={k}", flush=True)
         a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
         b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
