@@ -125,6 +125,29 @@ int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
 size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,
                               int with_argmax);
 
+/* Name of the kernel path tg_gemm_ws would run for this problem with a
+ * workspace of workspace_bytes (tg_gemm passes tg_gemm_workspace_size), e.g.
+ * "dl_4x8_cl16", "shortk", "tiles_exact" or "dl_4x4_cl8 split 2"; "invalid"
+ * for arguments the call would reject, "none" for an empty product.  Strides
+ * 0 mean dense single products.  Pure host logic: pointers are only checked
+ * for alignment, never dereferenced, and no device is needed.  Diagnostic,
+ * with no counterpart in the reference (which has one kernel per dtype). */
+const char* tg_gemm_plan(tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                         const void* A, const void* B, const void* C, const int32_t* argmax,
+                         int64_t batch, int64_t m, int64_t n, int64_t k,
+                         int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                         size_t workspace_bytes);
+
+/* Launch geometry the backward entry points would use for a gradient
+ * (want_a: 1 for grad A, 0 for grad B), e.g. "rows lds waves=2 lds=32768
+ * grid=2048": the kernel family (rows / cols), where the bins live (LDS, or
+ * the gradient itself for very large k), waves per workgroup, dynamic LDS
+ * bytes and workgroups.  Grids are capped (the kernels loop with a grid
+ * stride), so no launch dimension grows with m, n or batch.  Host logic
+ * only; diagnostic, with no counterpart in the reference. */
+const char* tg_backward_plan(tg_dtype dtype, tg_layout layout, int want_a, int64_t batch,
+                             int64_t m, int64_t n, int64_t k);
+
 /* tg_gemm with a caller-provided workspace of at least
  * tg_gemm_workspace_size(...) bytes, 256-byte aligned (no allocation). */
 int tg_gemm_ws(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,

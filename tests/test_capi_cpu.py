@@ -115,3 +115,49 @@ def test_python_layer_rejects_host_tensors():
         ops.gemm("maxplus", a, torch.zeros(3))
     with pytest.raises(ValueError, match="same dtype"):
         ops.gemm("maxplus", a, torch.zeros(3, 2, dtype=torch.float64))
+
+
+# ---------------------------------------------------------------------------
+# Dispatch and launch geometry (host logic; no device needed)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("sr,dt,m,n,k,argmax,expected", [
+    ("maxplus", "f32", 4096, 4096, 4096, True, "dl_4x8_cl16"),       # P
+    ("minplus", "f32", 4096, 4096, 4096, True, "dl_4x8_cl16"),       # C2
+    ("maxmul", "f32", 8192, 4096, 2048, False, "dl_8x8_cl32"),       # C3
+    ("maxplus", "i32", 262144, 128, 128, True, "kres8"),             # C4
+    ("maxplus", "f32", 1024, 1024, 1024, True, "dl_4x4_cl8 split 4"),  # C1
+    ("maxplus", "f32", 65536, 8, 2048, True, "shortk"),              # M1 (m, k, n order below)
+    ("maxplus", "f32", 67, 45, 40, True, "tiles_exact"),
+    ("maxplus", "f64", 4096, 4096, 4096, True, "tiles_chunked"),
+])
+def test_gemm_plan_names_the_configured_paths(sr, dt, m, n, k, argmax, expected):
+    if expected == "shortk":
+        m, n, k = 65536, 2048, 8
+    assert nat.gemm_plan(sr, dt, m, n, k, argmax) == expected
+
+
+def test_gemm_plan_rejects_what_the_call_rejects():
+    assert nat.gemm_plan("maxplus", "f32", -1, 4, 4) == "invalid"
+    assert nat.gemm_plan("maxplus", "f32", 0, 4, 4) == "none"
+
+
+@pytest.mark.parametrize("dt", [0, 1])
+@pytest.mark.parametrize("want_a", [1, 0])
+@pytest.mark.parametrize("shape", [(1, 4096, 4096, 4096), (1, (1 << 24) + 1, 2, 3),
+                                   (1, 3, (1 << 31) - 1, 3), (65535 * 4, 64, 64, 64),
+                                   (1, 5, 9000, 100000), (3, 2, 2, 1 << 30)])
+def test_backward_geometry_caps_every_launch_dimension(dt, want_a, shape):
+    """Grid-stride kernels: whatever M, N, K and batch, the grid stays at or
+    below 16384 workgroups of at most 512 threads, and LDS within the CU."""
+    batch, m, n, k = shape
+    lib = nat.load()
+    for layout in (0, 1):
+        plan = lib.tg_backward_plan(dt, layout, want_a, batch, m, n, k).decode()
+        fields = dict(f.split("=") for f in plan.split()[2:])
+        assert 1 <= int(fields["grid"]) <= 16384, plan
+        assert 1 <= int(fields["waves"]) <= 8, plan
+        assert int(fields["lds"]) <= 160 * 1024, plan
+        elem = 4 if dt == 0 else 8
+        if k * elem > 128 * 1024:
+            assert "global" in plan, plan

@@ -213,3 +213,55 @@ def test_avx2_value_baseline_equals_oracle(sr):
     z = oracle.avx2_gemm_f32(sr, np.zeros((3, 0), np.float32), np.zeros((0, 5), np.float32))
     np.testing.assert_array_equal(z, np.full((3, 5), {"maxplus": -np.inf, "minplus": np.inf,
                                                       "maxmul": 0.0}[sr], np.float32))
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_oracle_nan_closed_forms(sr, dtype):
+    """NaN products under the reference's keep-rule (acc >= p for max,
+    acc <= p for min): a NaN product replaces the running value and the next
+    product replaces the NaN, so a row's result is the first optimum of the
+    products after its last NaN product, or (NaN, that k) when the NaN comes
+    last; rows whose last product is NaN end NaN, and a product that only
+    ties the pre-NaN optimum after the reset still wins (no memory survives
+    the NaN).  Checked one output per row, k = 0..5, with A[i, k] the product
+    itself (B = the semiring's one), against the closed form, not the loop."""
+    one = 1.0 if sr == "maxmul" else 0.0
+    nan = np.nan
+    rows = [
+        [1, nan, 3, 2, 3, 0],    # reset at 1, then first optimum of [3, 2, 3, 0]
+        [5, 4, 3, 2, 1, nan],    # NaN last: (NaN, 5)
+        [nan, 2, 2, 1, 0, 2],    # NaN first: first optimum of the rest
+        [9, 1, nan, 1, 0, 0.5],  # the pre-NaN 9 is forgotten
+        [nan, nan, nan, nan, nan, 7],
+        [2, 2, 2, 2, 2, 2],      # no NaN: first optimum, k = 0
+    ]
+    if sr == "maxmul":
+        rows = [[abs(x) if x == x else x for x in r] for r in rows]
+    a = np.array(rows, dtype=dtype)
+    b = np.full((a.shape[1], 1), one, dtype=dtype)
+    c, am = oracle.gemm(sr, a, b)
+    better = (lambda x, y: x < y) if sr == "minplus" else (lambda x, y: x > y)
+    for i, r in enumerate(rows):
+        last_nan = max([k for k, x in enumerate(r) if x != x], default=-1)
+        if last_nan == len(r) - 1:
+            assert np.isnan(c[i, 0]) and am[i, 0] == last_nan
+            continue
+        tail = list(range(last_nan + 1, len(r)))
+        best = tail[0]
+        for k in tail[1:]:
+            if better(r[k], r[best]):
+                best = k
+        assert c[i, 0] == dtype(r[best]) and am[i, 0] == best, (i, c[i, 0], am[i, 0], best)
+
+
+def test_oracle_nan_from_infinities():
+    """-inf + inf and 0 * inf are NaN products: the same reset."""
+    a = np.array([[3.0, -np.inf, 1.0, 0.5]], dtype=np.float32)
+    b = np.array([[0.0], [np.inf], [0.0], [0.0]], dtype=np.float32)
+    c, am = oracle.gemm("maxplus", a, b)
+    assert c[0, 0] == 1.0 and am[0, 0] == 2          # 3 forgotten after the NaN at k = 1
+    a = np.array([[0.5, 0.0, 0.25, 0.125]], dtype=np.float32)
+    b = np.array([[1.0], [np.inf], [1.0], [1.0]], dtype=np.float32)
+    c, am = oracle.gemm("maxmul", a, b)
+    assert c[0, 0] == 0.25 and am[0, 0] == 2

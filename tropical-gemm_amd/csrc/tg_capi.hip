@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/tropical_gemm_hip.h"
+#include "tg_backward.hpp"
 #include "tg_gemm_dl.hpp"
 #include "tg_gemm_kres.hpp"
 #include "tg_gemm_kres8.hpp"
@@ -200,9 +201,9 @@ WsLayout ws_layout(tg_dtype dt, int64_t batch, int64_t M, int64_t N, int64_t K, 
 // Direct-to-LDS kernel for 32-bit types (partial edge tiles allowed, see
 // tg::dl_fits).  splits > 1 (full tiles only) runs K in that many slices into
 // the workspace partials, then merges them.
-template <int SR, typename T, int TN, int CL>
+template <int SR, typename T, int TM, int TN, int CL>
 int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
-    using Cfg = tg::DlCfg<TN>;
+    using Cfg = tg::DlCfg<TM, TN>;
     const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;  // the last ones may be partial
     const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
     if (tiles_m * tiles_n > 0x7fffffffLL)
@@ -231,6 +232,14 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
             TG_HIP(hipGetLastError());
         }
     }
+    // 128 x 128 value-only tiles take 64 KB of dynamic LDS: raise the
+    // kernel's limit once (no stream work, so also fine under capture).
+    if constexpr (Cfg::TILE_BYTES > 48 * 1024) {
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, false, TM, TN, CL>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::TILE_BYTES);
+        TG_HIP(attr);
+    }
     KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
         const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
@@ -244,33 +253,39 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         const bool tailk = p.K % Cfg::BK != 0;  // the last k-tile is partial
         if (argmax) {
             const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
-            if (tailk) {
-                // 64 x 64 tiles only: the 64 x 128 kernel with the tail code
-                // would spill (the plan never picks it for a partial K).
-                if constexpr (TN == 4)
-                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL, true>), grid,
-                                       dim3(256), Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M,
-                                       p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS,
-                                       sY);
-                else
-                    return fail(TG_ERR_INVALID_ARGUMENT, "internal: 64x128 tiles need K % 32 == 0");
-            } else
-                hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TN, CL>), grid, dim3(256),
-                                   Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA,
-                                   p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
+            if constexpr (TM == 4 && (Cfg::BK / CL) % 2 == 0) {
+                if (tailk) {
+                    // 64 x 64 tiles only: the 64 x 128 kernel with the tail
+                    // code would spill (the plan never picks it for a partial K).
+                    if constexpr (TN == 4)
+                        hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, true>), grid,
+                                           dim3(256), Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M,
+                                           p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n),
+                                           KS, sY);
+                    else
+                        return fail(TG_ERR_INVALID_ARGUMENT,
+                                    "internal: 64x128 tiles need K % 32 == 0");
+                } else
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL>), grid, dim3(256),
+                                       Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz, p.M, p.N, p.K,
+                                       p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
+            } else {
+                return fail(TG_ERR_INVALID_ARGUMENT,
+                            "internal: argmax tiles have 4 rows and an even chunk count per k-tile");
+            }
         } else {
             if (tailk) {
-                if constexpr (TN == 4)
-                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL, true>), grid,
-                                       dim3(256), Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz, nullptr,
-                                       p.M, p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n),
-                                       KS, sY);
+                if constexpr (TM == 4 && TN == 4)
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TM, TN, CL, true>), grid,
+                                       dim3(256), Cfg::TILE_BYTES, st, Az, Bz, nullptr, Cz,
+                                       nullptr, p.M, p.N, p.K, p.sA, p.sB, sCk, int(tiles_m),
+                                       int(tiles_n), KS, sY);
                 else
-                    return fail(TG_ERR_INVALID_ARGUMENT, "internal: 64x128 tiles need K % 32 == 0");
+                    return fail(TG_ERR_INVALID_ARGUMENT, "internal: wide tiles need K % 32 == 0");
             } else
-                hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TN, CL>), grid, dim3(256),
-                                   Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz, nullptr, p.M, p.N, p.K,
-                                   p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
+                hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TM, TN, CL>), grid, dim3(256),
+                                   Cfg::TILE_BYTES, st, Az, Bz, nullptr, Cz, nullptr, p.M, p.N,
+                                   p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS, sY);
         }
         TG_HIP(hipGetLastError());
     }
@@ -278,12 +293,15 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         const int64_t nvec = p.batch * MN / 4;
         int64_t blocks = (nvec + 255) / 256;
         if (blocks > 8192) blocks = 8192;
+        const T* BT = argmax ? reinterpret_cast<const T*>(wsb + wl.bt) : nullptr;
         if (argmax)
             hipLaunchKernelGGL((tg::tg_merge_splits<SR, T, true>), dim3(unsigned(blocks)), dim3(256), 0,
-                               st, PV, PI, C, p.IDX, splits, MN, p.batch, sY, p.sC);
+                               st, PV, PI, C, p.IDX, splits, MN, p.batch, sY, p.sC, A, B, BT, p.N,
+                               p.K, p.sA, p.sB);
         else
             hipLaunchKernelGGL((tg::tg_merge_splits<SR, T, false>), dim3(unsigned(blocks)), dim3(256), 0,
-                               st, PV, nullptr, C, nullptr, splits, MN, p.batch, sY, p.sC);
+                               st, PV, nullptr, C, nullptr, splits, MN, p.batch, sY, p.sC, A, B,
+                               BT, p.N, p.K, p.sA, p.sB);
         TG_HIP(hipGetLastError());
     }
     return TG_OK;
@@ -465,7 +483,7 @@ constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
 // The kernel a problem runs on.
-enum class Path { SHORTK, KRES8, KRES, DL_8_16, DL_4_8, DL_4_16, DL_4_32, TILES_EXACT, TILES_CHUNKED, TILES };
+enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, TILES_EXACT, TILES_CHUNKED, TILES };
 
 struct Plan {
     Path path = Path::TILES;
@@ -512,7 +530,7 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
         // Partial tiles (M, N or K): short argmax problems take the generic
         // kernel's exact mode (no resolve); longer ones and value-only run
         // the direct-to-LDS kernels with clamped loads.
-        const bool partial = !tg::dl_full_tiles<4>(p.M, p.N, p.K);
+        const bool partial = !tg::dl_full_tiles<4, 4>(p.M, p.N, p.K);
         // Value-only with K below 64 and not a multiple of 32: most of the
         // direct-to-LDS kernel's padded last k-tile would be wasted work;
         // the generic kernel bounds its last tile instead.
@@ -540,27 +558,37 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             // (their main loop is the faster one); 64 x 64 tiles otherwise
             // (value-only runs four workgroups per CU, small problems get
             // twice the tiles).
-            const bool wide = splits == 1 && argmax && cl == 16 && p.N % tg::DlCfg<8>::BN == 0 &&
-                              p.K % tg::DlCfg<8>::BK == 0 &&
-                              ((p.M + tg::DlCfg<8>::BM - 1) / tg::DlCfg<8>::BM) *
-                                      (p.N / tg::DlCfg<8>::BN) * p.batch >=
-                                  1536;
+            using W48 = tg::DlCfg<4, 8>;
+            using W88 = tg::DlCfg<8, 8>;
+            const bool wide = splits == 1 && argmax && cl == 16 && p.N % W48::BN == 0 &&
+                              p.K % W48::BK == 0 &&
+                              ((p.M + W48::BM - 1) / W48::BM) * (p.N / W48::BN) * p.batch >= 1536;
+            // Value-only problems with at least two rounds of 128 x 128 tiles
+            // (512 resident workgroups) run 8 x 8 outputs per thread.
+            const bool big = splits == 1 && !argmax && p.K % W88::BK == 0 &&
+                             ((p.M + W88::BM - 1) / W88::BM) * ((p.N + W88::BN - 1) / W88::BN) *
+                                     p.batch >= 1024;
             pl.splits = splits;
-            if (wide && tg::dl_fits<8, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
-                pl.path = Path::DL_8_16;
+            if (wide && tg::dl_fits<16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_48_16;
                 pl.splits = 1;
                 return pl;
             }
-            if (cl == 8 && tg::dl_fits<4, 8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
-                pl.path = Path::DL_4_8;
+            if (big && tg::dl_fits<32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_88_32;
+                pl.splits = 1;
                 return pl;
             }
-            if (cl == 16 && tg::dl_fits<4, 16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
-                pl.path = Path::DL_4_16;
+            if (cl == 8 && tg::dl_fits<8>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_44_8;
                 return pl;
             }
-            if (cl == 32 && tg::dl_fits<4, 32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
-                pl.path = Path::DL_4_32;
+            if (cl == 16 && tg::dl_fits<16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_44_16;
+                return pl;
+            }
+            if (cl == 32 && tg::dl_fits<32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_44_32;
                 return pl;
             }
             pl.splits = 1;
@@ -586,10 +614,11 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
                     return run_gemm_kres8<SR>(p, st);
                 break;
             case Path::KRES: return run_gemm_kres<SR, T>(p, st);
-            case Path::DL_8_16: return run_gemm_dl<SR, T, 8, 16>(p, ws, 1, st);
-            case Path::DL_4_8: return run_gemm_dl<SR, T, 4, 8>(p, ws, pl.splits, st);
-            case Path::DL_4_16: return run_gemm_dl<SR, T, 4, 16>(p, ws, pl.splits, st);
-            case Path::DL_4_32: return run_gemm_dl<SR, T, 4, 32>(p, ws, pl.splits, st);
+            case Path::DL_88_32: return run_gemm_dl<SR, T, 8, 8, 32>(p, ws, 1, st);
+            case Path::DL_48_16: return run_gemm_dl<SR, T, 4, 8, 16>(p, ws, 1, st);
+            case Path::DL_44_8: return run_gemm_dl<SR, T, 4, 4, 8>(p, ws, pl.splits, st);
+            case Path::DL_44_16: return run_gemm_dl<SR, T, 4, 4, 16>(p, ws, pl.splits, st);
+            case Path::DL_44_32: return run_gemm_dl<SR, T, 4, 4, 32>(p, ws, pl.splits, st);
             default: break;
         }
     }
@@ -693,6 +722,23 @@ Plan plan_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, size_t ws_bytes) {
     return Plan{};
 }
 
+const char* path_name(Path path) {
+    switch (path) {
+        case Path::SHORTK: return "shortk";
+        case Path::KRES8: return "kres8";
+        case Path::KRES: return "kres";
+        case Path::DL_88_32: return "dl_8x8_cl32";
+        case Path::DL_48_16: return "dl_4x8_cl16";
+        case Path::DL_44_8: return "dl_4x4_cl8";
+        case Path::DL_44_16: return "dl_4x4_cl16";
+        case Path::DL_44_32: return "dl_4x4_cl32";
+        case Path::TILES_EXACT: return "tiles_exact";
+        case Path::TILES_CHUNKED: return "tiles_chunked";
+        case Path::TILES: return "tiles";
+    }
+    return "?";
+}
+
 int run_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, void* ws, size_t ws_bytes,
              hipStream_t st) {
     switch (sr) {
@@ -761,6 +807,25 @@ int validate_forward(int sr, int dt, int layout, const void* A, const void* B, c
     return TG_OK;
 }
 
+// Layout mapping: a column-major product C = A (x) B is the row-major
+// product C^T = B^T (x) A^T over the same buffers (kernels.rs:370-430).
+Problem make_problem(tg_layout layout, const void* A, const void* B, void* C, int32_t* argmax,
+                     int64_t batch, int64_t m, int64_t n, int64_t k, int64_t sa, int64_t sb,
+                     int64_t sc, bool strided) {
+    Problem p;
+    if (layout == TG_ROW_MAJOR) {
+        p = Problem{A, B, C, argmax, batch, m, n, k, sa, sb, sc};
+    } else {
+        p = Problem{B, A, C, argmax, batch, n, m, k, sb, sa, sc};
+    }
+    if (!strided) {
+        p.sA = p.M * p.K;
+        p.sB = p.K * p.N;
+        p.sC = p.M * p.N;
+    }
+    return p;
+}
+
 int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const void* A,
               const void* B, void* C, int32_t* argmax, int64_t batch, int64_t m, int64_t n,
               int64_t k, int64_t sa, int64_t sb, int64_t sc, bool strided, void* ws,
@@ -784,19 +849,7 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
     if (batch == 0 || m == 0 || n == 0) return TG_OK;
     hipStream_t st = as_stream(stream);
 
-    // Layout mapping: a column-major product C = A (x) B is the row-major
-    // product C^T = B^T (x) A^T over the same buffers (kernels.rs:370-430).
-    Problem p;
-    if (layout == TG_ROW_MAJOR) {
-        p = Problem{A, B, C, argmax, batch, m, n, k, sa, sb, sc};
-    } else {
-        p = Problem{B, A, C, argmax, batch, n, m, k, sb, sa, sc};
-    }
-    if (!strided) {
-        p.sA = p.M * p.K;
-        p.sB = p.K * p.N;
-        p.sC = p.M * p.N;
-    }
+    Problem p = make_problem(layout, A, B, C, argmax, batch, m, n, k, sa, sb, sc, strided);
 
     // The kernels stage B^T (K x p.N per batch item) in the workspace.
     if (need > 0 && need < size_t(p.batch) * size_t(p.K) * size_t(p.N) * size_t(elem_size(dt)))
@@ -825,88 +878,109 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
 // Backward
 // ----------------------------------------------------------------------------
 
-constexpr size_t kRowLdsLimit = 64 * 1024;
+// Launch geometry of the deterministic backward kernels (tg_backward.hpp).
+// Both kernels loop over their rows / column groups with a grid stride, so
+// the grid is capped (kBwdMaxGrid workgroups) and no dimension of a launch
+// grows with M, N or the batch.
+constexpr int64_t kBwdMaxGrid = 16384;
+constexpr size_t kBwdLdsBudget = 128 * 1024;  // per workgroup, of the CU's 160 KB
+
+struct BwdGeometry {
+    bool global = false;  // bins in the gradient itself (K too large for LDS)
+    int waves = 1;        // waves per workgroup
+    size_t lds = 0;       // dynamic LDS bytes per workgroup
+    int64_t grid = 0;     // workgroups
+    int64_t groups_n = 0; // grad_B: column groups per batch item
+    int64_t groups = 0;   // grad_B: column groups in total
+};
+
+// grad_A: one wave per row; two waves per workgroup (32 KB of bins each at
+// K = 4096 f32, five workgroups per CU), one wave when a row's bins need
+// more than 64 KB, global bins beyond the LDS budget.
+BwdGeometry bwd_rows_geometry(int64_t rows, int64_t K, size_t es) {
+    BwdGeometry g;
+    const size_t row_bytes = size_t(K) * es;
+    if (row_bytes <= 32 * 1024) {
+        g.waves = 2;
+    } else if (row_bytes <= kBwdLdsBudget) {
+        g.waves = 1;
+    } else {
+        g.global = true;
+        g.waves = 4;
+    }
+    g.lds = g.global ? 0 : size_t(g.waves) * row_bytes;
+    const int64_t need = (rows + g.waves - 1) / g.waves;
+    g.grid = need < kBwdMaxGrid ? need : kBwdMaxGrid;
+    return g;
+}
+
+// grad_B: one wave per column, W <= 8 adjacent columns per workgroup, as
+// many as their bins fit the LDS budget (8 at K = 4096 f32), plus the staged
+// 64 x W tiles of argmax and dC.
+BwdGeometry bwd_cols_geometry(int64_t batch, int64_t N, int64_t K, size_t es) {
+    BwdGeometry g;
+    const size_t col_bytes = size_t(K) * es;
+    int64_t w = col_bytes > 0 ? int64_t(kBwdLdsBudget / col_bytes) : 8;
+    if (w > 8) w = 8;
+    if (w < 1) {
+        g.global = true;
+        w = 8;
+    }
+    g.waves = int(w);
+    g.lds = (g.global ? 0 : size_t(w) * col_bytes) + 64 * size_t(w + 1) * (4 + es);
+    g.groups_n = (N + w - 1) / w;
+    g.groups = batch * g.groups_n;
+    g.grid = g.groups < kBwdMaxGrid ? g.groups : kBwdMaxGrid;
+    return g;
+}
+
+// Raises a kernel's dynamic LDS limit once (needed above 64 KB).
+template <typename K>
+int allow_lds(K* kernel, size_t bytes) {
+    if (bytes <= 64 * 1024) return TG_OK;
+    TG_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
+    return TG_OK;
+}
 
 template <typename T, bool MULT>
 int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sA, hipStream_t st) {
-    for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
-        const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
-        const T* Gz = G + z0 * sC;
-        const int32_t* Iz = I + z0 * sC;
-        const T* Oz = MULT ? O + z0 * sO : nullptr;
-        T* GAz = GA + z0 * sA;
-        const size_t lds = size_t(K) * sizeof(T);
-        if (lds <= kRowLdsLimit && M <= 0x7fffffffLL) {
-            hipLaunchKernelGGL((tg::tg_backward_rows<T, MULT>), dim3(unsigned(M), 1, unsigned(nb)),
-                               dim3(256), lds, st, Gz, Iz, Oz, GAz, M, N, K, sC, sO, sA);
-            TG_HIP(hipGetLastError());
-        } else {
-            for (int64_t z = 0; z < nb; ++z) {
-                int rc = launch_fill_zero(GAz + z * sA, size_t(M * K) * sizeof(T), st);
-                if (rc != TG_OK) return rc;
-            }
-            const int64_t blocks = (M * N + 255) / 256;
-            hipLaunchKernelGGL((tg::tg_backward_rows_global<T, MULT>),
-                               dim3(unsigned(blocks), 1, unsigned(nb)), dim3(256), 0, st, Gz, Iz,
-                               Oz, GAz, M, N, K, sC, sO, sA);
-            TG_HIP(hipGetLastError());
-        }
+    const BwdGeometry g = bwd_rows_geometry(batch * M, K, sizeof(T));
+    if (g.grid == 0) return TG_OK;
+    if (g.global) {
+        hipLaunchKernelGGL((tg::tg_bwd_rows<T, MULT, true>), dim3(unsigned(g.grid)),
+                           dim3(64 * g.waves), 0, st, G, I, O, GA, M, N, K, sC, sO, sA, batch * M);
+    } else {
+        int rc = allow_lds(&tg::tg_bwd_rows<T, MULT, false>, g.lds);
+        if (rc != TG_OK) return rc;
+        hipLaunchKernelGGL((tg::tg_bwd_rows<T, MULT, false>), dim3(unsigned(g.grid)),
+                           dim3(64 * g.waves), g.lds, st, G, I, O, GA, M, N, K, sC, sO, sA,
+                           batch * M);
     }
+    TG_HIP(hipGetLastError());
     return TG_OK;
 }
-
-// LDS capacities (elements) of the two column-block kernel variants.
-template <typename T>
-struct ColsLds {
-    static constexpr int SMALL = 32768 / int(sizeof(T));   // 32 KB: several workgroups per CU
-    static constexpr int LARGE = 131072 / int(sizeof(T));  // 128 KB: one workgroup per CU
-};
 
 template <typename T, bool MULT>
 int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sB, hipStream_t st) {
-    // Column block: the widest power of two <= 64 whose K x BJ block fits.
-    auto block_log2 = [&](int64_t cap) {
-        int l = 0;
-        while (l < 6 && K * (int64_t(2) << l) <= cap) ++l;
-        return K <= cap ? l : -1;
-    };
-    int lsmall = block_log2(ColsLds<T>::SMALL);
-    int llarge = block_log2(ColsLds<T>::LARGE);
-    const bool use_small = lsmall >= 3;  // at least 8 columns per block
-    const int l = use_small ? lsmall : llarge;
-    if (l < 0) {
-        // K too large for LDS blocks: global atomics into a zeroed grad_B.
-        for (int64_t z = 0; z < batch; ++z) {
-            int rc = launch_fill_zero(GB + z * sB, size_t(K * N) * sizeof(T), st);
-            if (rc != TG_OK) return rc;
-        }
-        if (M * N == 0) return TG_OK;
-        for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
-            const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
-            const int64_t blocks = (M * N + 255) / 256;
-            hipLaunchKernelGGL((tg::tg_backward_cols<T, MULT>), dim3(unsigned(blocks), 1, unsigned(nb)),
-                               dim3(256), 0, st, G + z0 * sC, I + z0 * sC,
-                               MULT ? O + z0 * sO : nullptr, GB + z0 * sB, M, N, K, sC, sO, sB);
-            TG_HIP(hipGetLastError());
-        }
-        return TG_OK;
+    const BwdGeometry g = bwd_cols_geometry(batch, N, K, sizeof(T));
+    if (g.grid == 0) return TG_OK;
+    if (g.global) {
+        int rc = allow_lds(&tg::tg_bwd_cols<T, MULT, true>, g.lds);
+        if (rc != TG_OK) return rc;
+        hipLaunchKernelGGL((tg::tg_bwd_cols<T, MULT, true>), dim3(unsigned(g.grid)),
+                           dim3(64 * g.waves), g.lds, st, G, I, O, GB, M, N, K, sC, sO, sB,
+                           g.groups_n, g.groups);
+    } else {
+        int rc = allow_lds(&tg::tg_bwd_cols<T, MULT, false>, g.lds);
+        if (rc != TG_OK) return rc;
+        hipLaunchKernelGGL((tg::tg_bwd_cols<T, MULT, false>), dim3(unsigned(g.grid)),
+                           dim3(64 * g.waves), g.lds, st, G, I, O, GB, M, N, K, sC, sO, sB,
+                           g.groups_n, g.groups);
     }
-    const int64_t nblocks = (N + (int64_t(1) << l) - 1) >> l;
-    for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
-        const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
-        const T* Oz = MULT ? O + z0 * sO : nullptr;
-        if (use_small)
-            hipLaunchKernelGGL((tg::tg_backward_cols_lds<T, MULT, ColsLds<T>::SMALL>),
-                               dim3(unsigned(nblocks), 1, unsigned(nb)), dim3(512), 0, st, G + z0 * sC,
-                               I + z0 * sC, Oz, GB + z0 * sB, M, N, K, sC, sO, sB, l);
-        else
-            hipLaunchKernelGGL((tg::tg_backward_cols_lds<T, MULT, ColsLds<T>::LARGE>),
-                               dim3(unsigned(nblocks), 1, unsigned(nb)), dim3(512), 0, st, G + z0 * sC,
-                               I + z0 * sC, Oz, GB + z0 * sB, M, N, K, sC, sO, sB, l);
-        TG_HIP(hipGetLastError());
-    }
+    TG_HIP(hipGetLastError());
     return TG_OK;
 }
 
@@ -1138,6 +1212,41 @@ size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t 
                               int with_argmax) {
     if (!valid_dtype(dtype)) return 0;
     return workspace_bytes_for(dtype, batch, m, n, k, with_argmax != 0);
+}
+
+const char* tg_gemm_plan(tg_semiring semiring, tg_dtype dtype, tg_layout layout, const void* A,
+                         const void* B, const void* C, const int32_t* argmax, int64_t batch,
+                         int64_t m, int64_t n, int64_t k, int64_t stride_a, int64_t stride_b,
+                         int64_t stride_c, size_t workspace_bytes) {
+    static thread_local std::string name;
+    const bool strided = stride_a != 0 || stride_b != 0 || stride_c != 0;
+    if (validate_forward(semiring, dtype, layout, A, B, C, batch, m, n, k, stride_a, stride_b,
+                         stride_c, strided) != TG_OK)
+        return "invalid";
+    if (batch == 0 || m == 0 || n == 0) return "none";
+    const Problem p = make_problem(layout, A, B, const_cast<void*>(C), const_cast<int32_t*>(argmax),
+                                   batch, m, n, k, stride_a, stride_b, stride_c, strided);
+    const Plan pl = plan_gemm(semiring, dtype, p, workspace_bytes);
+    name = path_name(pl.path);
+    if (pl.splits > 1) name += " split " + std::to_string(pl.splits);
+    return name.c_str();
+}
+
+const char* tg_backward_plan(tg_dtype dtype, tg_layout layout, int want_a, int64_t batch,
+                             int64_t m, int64_t n, int64_t k) {
+    static thread_local std::string name;
+    if ((dtype != TG_F32 && dtype != TG_F64) || !valid_layout(layout) || batch < 0 || m < 0 ||
+        n < 0 || k < 0)
+        return "invalid";
+    const size_t es = size_t(elem_size(dtype));
+    // Row-major problem after the layout mapping (see backward_impl).
+    const bool rows = (layout == TG_ROW_MAJOR) == (want_a != 0);
+    const int64_t M = layout == TG_ROW_MAJOR ? m : n, N = layout == TG_ROW_MAJOR ? n : m;
+    const BwdGeometry g = rows ? bwd_rows_geometry(batch * M, k, es) : bwd_cols_geometry(batch, N, k, es);
+    name = std::string(rows ? "rows" : "cols") + (g.global ? " global" : " lds") +
+           " waves=" + std::to_string(g.waves) + " lds=" + std::to_string(g.lds) +
+           " grid=" + std::to_string(g.grid);
+    return name.c_str();
 }
 
 int tg_gemm_ws(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout, const void* A,

@@ -1,55 +1,58 @@
 // tg_gemm_dl.hpp -- direct-to-LDS tropical GEMM for 32-bit types (gfx950).
 //
-// Same contract as tg_gemm_tiles (tg_kernels.hpp), for problems whose tiles
-// are all full: M % 64 == 0, N % 128 == 0, K % 32 == 0, 16-byte aligned A, B
-// and batch strides.  Tiles go from HBM straight into LDS with
-// global_load_lds_dwordx4 (no staging registers, no LDS-store VALU work),
-// which frees the registers the argmax bookkeeping needs and keeps three
-// waves per SIMD resident.
+// Same contract as tg_gemm_tiles (tg_kernels.hpp).  Tiles go from HBM
+// straight into LDS with global_load_lds_dwordx4 (no staging registers, no
+// LDS-store VALU work), which frees the registers the argmax bookkeeping
+// needs.
 //
-// Layouts (per LDS buffer; two buffers, loads of chunk t+1 overlap the
-// compute of chunk t):
-//   A tile  64 rows x 32 k, row-major (128 B rows).  The 16-byte quad q of
+// Layouts (per LDS buffer; two buffers, loads of k-tile t+1 overlap the
+// compute of k-tile t):
+//   A tile  BM rows x 32 k, row-major (128 B rows).  The 16-byte quad q of
 //           row r is stored at quad position q ^ ((r >> 2) & 7), so the four
 //           rows a wave reads at one k fall in different banks.
-//   B tile  32 k x 128 cols, row-major (512 B rows).
-// Each thread owns 4 consecutive rows (ty*4 + i) and 8 columns
-// (g*64 + tx*4 + e): per pair of k it reads four ds_read_b64 of A and four
-// ds_read_b128 of B for 64 products.
+//   B tile  32 k x BN cols, row-major.
+// 16 x 16 threads; thread (tx, ty) owns rows (i >> 2) * 64 + ty*4 + (i & 3)
+// for i < TM and columns (j >> 2) * 64 + tx*4 + (j & 3) for j < TN.  Per
+// pair of k it reads TM ds_read_b64 of A and TN/2 ds_read_b128 of B for
+// 2 TM TN products: 4 (TM + TN) / (TM TN) bytes of LDS per product (1.5 for
+// 4 x 8, 1 for 8 x 8).
 #pragma once
 
 #include "tg_kernels.hpp"
 
 namespace tg {
 
-// Tile configurations: 16 x 16 threads, 4 x TN outputs per thread.
-//   TN = 8: 64 x 128 tiles; argmax held to 3 waves/SIMD (<= 168 VGPRs),
-//           value-only at 2 (its schedule wants ~200 VGPRs).
-//   TN = 4: 64 x 64 tiles, 4 waves/SIMD (<= 128 VGPRs): twice the tiles, so
-//           4096^2 outputs make exactly 4 rounds of 1024 resident workgroups.
-template <int TN_>
+// Tile configurations, TM x TN outputs per thread:
+//   4 x 8: 64 x 128 tiles; argmax held to 3 waves/SIMD (<= 168 VGPRs),
+//          value-only at 2.
+//   4 x 4: 64 x 64 tiles, 4 waves/SIMD (<= 128 VGPRs): small problems, split
+//          K, partial k-tiles.
+//   8 x 8: 128 x 128 tiles, value-only, 2 waves/SIMD: 1 byte of LDS per
+//          product (MaxPlus f32 4096^3 value-only: 1.86 ms against 1.99 for
+//          4 x 8 and 2.04-2.14 for 4 x 4 on MI355X).
+template <int TM_, int TN_>
 struct DlCfg {
-    static constexpr int BM = 64, BN = 16 * TN_, BK = TG_CHUNK, TM = 4, TN = TN_;
+    static constexpr int TM = TM_, TN = TN_;
+    static constexpr int BM = 16 * TM_, BN = 16 * TN_, BK = TG_CHUNK;
     static constexpr int WAVES_ARGMAX = TN_ == 8 ? 3 : 4;
     static constexpr int WAVES_VALUE = TN_ == 8 ? 2 : 4;
+    static constexpr int NAI = BM * BK / 1024;      // 1 KB A-tile loads per wave
     static constexpr int NBI = BK * BN / 1024;      // 1 KB B-tile loads per wave
     static constexpr int RPI = 256 / BN;            // B k-rows per 1 KB load
     static constexpr int LPR = BN / 4;              // lanes per B k-row
     static constexpr int A_BYTES = BM * BK * 4;   // one A buffer
     static constexpr int B_BYTES = BK * BN * 4;   // one B buffer
     static constexpr int TILE_BYTES = 2 * (A_BYTES + B_BYTES);
-    // Argmax epilogue, reusing the tile buffers: bucket counts, per-output
-    // chunk (u16), chunk-sorted output list (u16), per-output result (u8),
-    // then a few words of scan scratch past the tile buffers.
+    // Argmax epilogue, reusing the tile buffers: bucket counts (then bucket
+    // cursors), per-output chunk (u16; the resolve overwrites it with its
+    // result), chunk-sorted output list (u16), a few words of scan scratch.
     static constexpr int OUTS = BM * BN;            // outputs per tile
-    static constexpr int NB_MAX = 2048;             // chunk buckets
+    static constexpr int NB = 256;                  // chunk buckets
     static constexpr int HIST_OFF = 0;
-    static constexpr int CHS_OFF = HIST_OFF + NB_MAX * 4;
+    static constexpr int CHS_OFF = HIST_OFF + NB * 4;
     static constexpr int LIST_OFF = CHS_OFF + OUTS * 2;
-    static constexpr int RES_OFF = LIST_OFF + OUTS * 2;
-    static constexpr int MISC_OFF = RES_OFF + OUTS;
+    static constexpr int MISC_OFF = LIST_OFF + OUTS * 2;
     static constexpr int LDS_BYTES = (MISC_OFF + 64 > TILE_BYTES) ? MISC_OFF + 64 : TILE_BYTES;
-    static_assert(MISC_OFF <= TILE_BYTES, "epilogue arrays must fit in the tile buffers");
 };
 
 // Exclusive prefix sum over the 256 threads of a workgroup; returns the
@@ -85,7 +88,7 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
-// True when tg_gemm_dl<.., TN, CL> can run the problem: K and N multiples of
+// True when tg_gemm_dl<.., CL> can run the problem: K and N multiples of
 // 4 and 16-byte aligned operands, outputs and batch strides (tiles load and
 // store 16 bytes per lane), and chunk indices that fit the epilogue's 16-bit
 // slots.  M, N and K need not fill the tiles: the loads of a partial tile
@@ -93,19 +96,19 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
 // the k past K of the last k-tile are then overwritten in LDS with operands
 // whose product is the tropical zero, and the stores skip rows past M and
 // 4-column groups past N.
-template <int TN, int CL>
+template <int CL>
 inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int64_t sC,
                     const void* A, const void* B, const void* C, const void* IDX) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     return M > 0 && N > 0 && K > 0 && N % 4 == 0 && K % 4 == 0 && (K + CL - 1) / CL < 0xFFFF &&
-           sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) &&
+           K < (int64_t(1) << 26) && N < (int64_t(1) << 28) && sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) &&
            (IDX == nullptr || a16(IDX));
 }
 
 // True when every tile of the problem is full.
-template <int TN>
+template <int TM, int TN>
 inline bool dl_full_tiles(int64_t M, int64_t N, int64_t K) {
-    return M % DlCfg<TN>::BM == 0 && N % DlCfg<TN>::BN == 0 && K % DlCfg<TN>::BK == 0;
+    return M % DlCfg<TM, TN>::BM == 0 && N % DlCfg<TM, TN>::BN == 0 && K % DlCfg<TM, TN>::BK == 0;
 }
 
 // Split K for problems with too few 64 x 64 tiles (partial ones included) to
@@ -124,7 +127,10 @@ inline int dl_splits(int64_t M, int64_t N, int64_t K, int64_t batch) {
 // Combines the S split-K partials of tg_gemm_dl.  Slices are visited in k
 // order and a later slice replaces the running result only if strictly
 // better, so equal values keep the earlier slice's index and bits: the
-// reference's first-k rule across slices.  Partials are dense, slice stride
+// reference's first-k rule across slices.  A slice whose chain met a NaN
+// product left NaN in its partial; such an output is recomputed here with
+// the reference's serial rule over the whole k range (A row, and B^T row
+// with argmax or B column without).  Partials are dense, slice stride
 // sY = batch * M * N; outputs use the batch stride sC.  16-byte vectors
 // (N, so M * N, is a multiple of 4 here).
 template <int SR, typename T, bool ARGMAX>
@@ -132,7 +138,10 @@ __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
                                                        const int32_t* __restrict__ PI,
                                                        T* __restrict__ C, int32_t* __restrict__ IDX,
                                                        int S, int64_t MN, int64_t batch, int64_t sY,
-                                                       int64_t sC) {
+                                                       int64_t sC, const T* __restrict__ A,
+                                                       const T* __restrict__ B,
+                                                       const T* __restrict__ BT, int64_t N,
+                                                       int64_t K, int64_t sA, int64_t sB) {
     const int64_t nvec = batch * MN / 4;
     const int64_t stride = int64_t(gridDim.x) * 256;
     for (int64_t v = int64_t(blockIdx.x) * 256 + threadIdx.x; v < nvec; v += stride) {
@@ -142,16 +151,33 @@ __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
         Vec16<T> best = *reinterpret_cast<const Vec16<T>*>(PV + e);
         Vec16<int32_t> bi{};
         if constexpr (ARGMAX) bi = *reinterpret_cast<const Vec16<int32_t>*>(PI + e);
+        bool nan[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) nan[q] = tisnan(best.v[q]);
         for (int y = 1; y < S; ++y) {
             const Vec16<T> pv = *reinterpret_cast<const Vec16<T>*>(PV + y * sY + e);
             Vec16<int32_t> pi{};
             if constexpr (ARGMAX) pi = *reinterpret_cast<const Vec16<int32_t>*>(PI + y * sY + e);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                nan[q] = nan[q] || tisnan(pv.v[q]);
                 if (tbetter<SR, T>(pv.v[q], best.v[q])) {
                     best.v[q] = pv.v[q];
                     if constexpr (ARGMAX) bi.v[q] = pi.v[q];
                 }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (nan[q]) {
+                const int64_t i = (r + q) / N, j = (r + q) - ((r + q) / N) * N;
+                const T* a = A + z * sA + i * K;
+                int32_t ix;
+                if constexpr (ARGMAX)
+                    cpu_select<SR, T>(a, 1, BT + z * (N * K) + j * K, 1, K, best.v[q], ix);
+                else
+                    cpu_select<SR, T>(a, 1, B + z * sB + j, N, K, best.v[q], ix);
+                if constexpr (ARGMAX) bi.v[q] = ix;
             }
         }
         *reinterpret_cast<Vec16<T>*>(C + z * sC + r) = best;
@@ -159,21 +185,56 @@ __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
     }
 }
 
+// Chunk records of four outputs: ch[q] = c where cand[q] strictly beats
+// prev[q] (the reference's keep-rule "acc >= p" for max, "acc <= p" for min,
+// types/max_plus.rs:66-73, min_plus.rs:66-73).  The four compares write four
+// SGPR masks before the four selects read them: compiled per output, each
+// compare went to VCC and its select waited two wait states on it (the
+// gfx950 VALU-mask hazard), which cost more than the compare itself.
+template <int SR, typename T>
+__device__ __forceinline__ void record4(int32_t& c0, int32_t& c1, int32_t& c2, int32_t& c3,
+                                        T n0, T n1, T n2, T n3, T p0, T p1, T p2, T p3,
+                                        int32_t cv) {
+    uint64_t m0, m1, m2, m3;
+#define TG_RECORD4_ASM(CMP)                                                                    \
+    asm volatile(CMP " %0, %8, %12\n\t" CMP " %1, %9, %13\n\t" CMP " %2, %10, %14\n\t" CMP    \
+                     " %3, %11, %15\n\t"                                                       \
+                     "v_cndmask_b32_e64 %4, %4, %16, %0\n\t"                                    \
+                     "v_cndmask_b32_e64 %5, %5, %16, %1\n\t"                                    \
+                     "v_cndmask_b32_e64 %6, %6, %16, %2\n\t"                                    \
+                     "v_cndmask_b32_e64 %7, %7, %16, %3"                                        \
+                 : "=&s"(m0), "=&s"(m1), "=&s"(m2), "=&s"(m3), "+v"(c0), "+v"(c1), "+v"(c2), \
+                   "+v"(c3)                                                                     \
+                 : "v"(n0), "v"(n1), "v"(n2), "v"(n3), "v"(p0), "v"(p1), "v"(p2), "v"(p3),      \
+                   "v"(cv))
+    if constexpr (std::is_same<T, float>::value) {
+        if constexpr (SR == SR_MINPLUS) TG_RECORD4_ASM("v_cmp_lt_f32_e64");
+        else TG_RECORD4_ASM("v_cmp_gt_f32_e64");
+    } else {
+        static_assert(std::is_same<T, int32_t>::value, "32-bit types only");
+        if constexpr (SR == SR_MINPLUS) TG_RECORD4_ASM("v_cmp_lt_i32_e64");
+        else TG_RECORD4_ASM("v_cmp_gt_i32_e64");
+    }
+#undef TG_RECORD4_ASM
+}
+
 // Waves per SIMD come from the tile configuration (DlCfg): other resident
 // waves hide the LDS latency of the main loop.
 // TAILK: K is not a multiple of BK (the last k-tile is partial); a separate
 // instantiation, so full-K problems run the plain pipeline.
-template <int SR, typename T, bool ARGMAX, int TN_, int CL, bool TAILK = false>
+template <int SR, typename T, bool ARGMAX, int TM_, int TN_, int CL, bool TAILK = false>
 __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
-    ARGMAX ? DlCfg<TN_>::WAVES_ARGMAX : DlCfg<TN_>::WAVES_VALUE))) void tg_gemm_dl(
+    ARGMAX ? DlCfg<TM_, TN_>::WAVES_ARGMAX : DlCfg<TM_, TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
     int64_t sB, int64_t sC, int tiles_m, int tiles_n, int64_t KS, int64_t sY) {
     static_assert(sizeof(T) == 4, "direct-to-LDS kernel is for 32-bit types");
-    using Cfg = DlCfg<TN_>;
+    using Cfg = DlCfg<TM_, TN_>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, TM = Cfg::TM, TN = Cfg::TN;
-    constexpr int NBI = Cfg::NBI;
+    constexpr int NAI = Cfg::NAI, NBI = Cfg::NBI;
     static_assert(CL == 8 || CL == 16 || CL == 32, "argmax chunk of 8, 16 or 32 k");
+    static_assert(!ARGMAX || (BK / CL) % 2 == 0, "argmax: an even number of chunks per k-tile");
+    static_assert(!ARGMAX || TM == 4, "argmax tiles have 4 rows per thread");
     extern __shared__ __align__(16) unsigned char dl_lds[];
     T* const As0 = reinterpret_cast<T*>(dl_lds);
     T* const Bs0 = reinterpret_cast<T*>(dl_lds + 2 * Cfg::A_BYTES);
@@ -199,38 +260,48 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         IDX += z * sC + y * sY;
         BT += z * (N * K);
     }
+    // Tile row / column of this thread's output (i, j).
+    auto trow = [&](int i) { return (i >> 2) * 64 + ty * 4 + (i & 3); };
+    auto tcol = [&](int j) { return (j >> 2) * 64 + tx * 4 + (j & 3); };
 
-    // Per-lane global sources of this wave's direct loads (chunk 0).  A: 8
-    // rows per 1 KB instruction, wave w issues instructions 2w, 2w+1.  B:
-    // RPI k-rows per instruction, wave w issues NBI*w .. NBI*w + NBI-1.  In a
-    // partial tile, rows past M read row M-1 and 4-column groups past N read
-    // the last group: in-bounds duplicates that only feed outputs that are
-    // never stored.
-    const T* srcA[2];
+    // Direct loads of k-tile t.  A: 8 rows per 1 KB instruction, wave w
+    // issues instructions NAI*w .. NAI*w + NAI-1; B: RPI k-rows per
+    // instruction, wave w issues NBI*w .. NBI*w + NBI-1.  Each address is a
+    // wave-uniform base (SGPRs) plus a 32-bit per-lane byte offset (a VGPR
+    // each for A, one for B), so the loads hold few registers through the
+    // main loop.  In a partial tile, rows past M read row M-1 and 4-column
+    // groups past N read the last group: in-bounds duplicates that only feed
+    // outputs that are never stored.  A base row: the first row of the
+    // instruction, clamped; the lane's row offset stays in [0, 7], so the
+    // offsets fit 32 bits for K < 2^26 (dl_fits).
+    uint32_t offA[NAI];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int r = (wave * 2 + q) * 8 + (lane >> 3);
-        const int qpos = lane & 7;
-        const int qsrc = qpos ^ ((r >> 2) & 7);
-        const int64_t gr = row0 + r < M ? row0 + r : M - 1;
-        srcA[q] = A + gr * K + qsrc * 4;
+    for (int q = 0; q < NAI; ++q) {
+        const int64_t rb = row0 + (wave * NAI + q) * 8;
+        const int64_t gr = rb + (lane >> 3);
+        const int r = int(gr - row0);
+        const int qsrc = (lane & 7) ^ ((r >> 2) & 7);
+        offA[q] = uint32_t(((gr < M ? gr : M - 1) - (rb < M ? rb : M - 1)) * K * 4 + qsrc * 16);
     }
-    const T* srcB[NBI];
-#pragma unroll
-    for (int q = 0; q < NBI; ++q) {
-        const int kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
-        const int64_t gc = col0 + (lane % Cfg::LPR) * 4;
-        srcB[q] = B + int64_t(kr) * N + (gc < N ? gc : N - 4);
-    }
+    auto a_base = [&](int q) {
+        const int64_t rb = row0 + (wave * NAI + q) * 8;
+        return reinterpret_cast<const unsigned char*>(A + (rb < M ? rb : M - 1) * K);
+    };
+    const int64_t gcB = col0 + (lane % Cfg::LPR) * 4;
+    const uint32_t offB =
+        uint32_t((lane / Cfg::LPR) * N * 4 + (gcB < N ? gcB : N - 4) * 4);
+    auto b_base = [&](int q, int64_t k0) {
+        return reinterpret_cast<const unsigned char*>(B + (k0 + (wave * NBI + q) * Cfg::RPI) * N);
+    };
     auto issue_loads = [&](int64_t t, int buf) {
         T* adst = As0 + buf * (BM * BK);
         T* bdst = Bs0 + buf * (BK * BN);
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
-            lds_load16(srcA[q] + t * BK, adst + (wave * 2 + q) * 256);
+        for (int q = 0; q < NAI; ++q)
+            lds_load16(a_base(q) + t * BK * 4 + offA[q], adst + (wave * NAI + q) * 256);
 #pragma unroll
         for (int q = 0; q < NBI; ++q)
-            lds_load16(srcB[q] + t * BK * N, bdst + (wave * NBI + q) * 256);
+            lds_load16(b_base(q, t * BK) + offB, bdst + (wave * NBI + q) * 256);
     };
     // The last k-tile when K is not a multiple of BK: A quads past K read the
     // row's last quad and B rows past K read row K-1 (in bounds; overwritten
@@ -239,17 +310,20 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         T* adst = As0 + buf * (BM * BK);
         T* bdst = Bs0 + buf * (BK * BN);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int r = (wave * 2 + q) * 8 + (lane >> 3);
+        for (int q = 0; q < NAI; ++q) {
+            const int r = (wave * NAI + q) * 8 + (lane >> 3);
             const int qsrc = (lane & 7) ^ ((r >> 2) & 7);
             const int64_t kq = t * BK + qsrc * 4;
-            lds_load16(srcA[q] - qsrc * 4 + (kq < K - 4 ? kq : K - 4), adst + (wave * 2 + q) * 256);
+            const int64_t kc = kq < K - 4 ? kq : K - 4;
+            lds_load16(a_base(q) + kc * 4 + (offA[q] - qsrc * 16), adst + (wave * NAI + q) * 256);
         }
 #pragma unroll
         for (int q = 0; q < NBI; ++q) {
             const int kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
             const int64_t kk = t * BK + kr;
-            lds_load16(srcB[q] - int64_t(kr) * N + (kk < K - 1 ? kk : K - 1) * N,
+            const int64_t kc = kk < K - 1 ? kk : K - 1;
+            lds_load16(reinterpret_cast<const unsigned char*>(B + kc * N) +
+                           (offB - uint32_t((lane / Cfg::LPR) * N * 4)),
                        bdst + (wave * NBI + q) * 256);
         }
     };
@@ -268,33 +342,73 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         for (int e = tid; e < nb; e += TG_THREADS) bs[kv * BN + e] = T(0);
     };
 
-    T acc[TM][TN];
+    // acc / alt: the running value, alternating between the two arrays from
+    // chunk to chunk (argmax: the chain of a chunk runs from one into the
+    // other, so the value held before the chunk is still there for the
+    // record, and no copies are needed).  ch: last chunk that strictly
+    // improved the output (-1: the tropical zero was never beaten).
+    T acc[TM][TN], alt[TM][TN];
     int32_t ch[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             acc[i][j] = tzero<SR, T>();
+            alt[i][j] = tzero<SR, T>();
             ch[i][j] = -1;
         }
 
-    // Fragment reads.  A: row ty*4+i, k pair (kk, kk+1) at its swizzled quad.
-    const int swz = ty & 7;
+    // Fragment reads.  A: row trow(i), k pair (kk, kk+1) at its swizzled quad.
+    // The swizzle of a thread's rows is ty & 7 for every i ((trow(i) >> 2) & 7);
+    // swz_t is re-declared opaque once per k-tile, so the eight swizzled quad
+    // offsets are recomputed per tile (a few VALU ops) instead of being held
+    // in registers through the loop.
+    int swz_t = ty & 7;
     auto load_frag = [&](int buf, int kk, T (&a)[TM][2], T (&b)[2][TN]) {
         const T* as = As0 + buf * (BM * BK);
         const T* bs = Bs0 + buf * (BK * BN);
+        const int q = (((kk >> 2) ^ swz_t) << 2) + (kk & 3);
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const int r = ty * 4 + i;
-            const int off = r * BK + (((kk >> 2) ^ swz) << 2) + (kk & 3);
+            const int off = trow(i) * BK + q;
             a[i][0] = as[off];
             a[i][1] = as[off + 1];
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                b[h][j] = bs[(kk + h) * BN + (j >> 2) * 64 + tx * 4 + (j & 3)];
+            for (int j = 0; j < TN; ++j) b[h][j] = bs[(kk + h) * BN + tcol(j)];
+    };
+    // One argmax chunk: the products of k in [s*CL, (s+1)*CL) of the tile in
+    // buffer buf fold into a max3/min3 chain that starts from `from` and ends
+    // in `to`; the chunk is recorded where `to` strictly beats `from`.
+    // Value-only: the chain runs in place (from and to are the same array).
+    auto chunk = [&](int64_t t, int buf, int s, const T (&from)[TM][TN], T (&to)[TM][TN]) {
+#pragma unroll
+        for (int kk = s * CL; kk < (s + 1) * CL; kk += 2) {
+            T a[TM][2], b[2][TN];
+            load_frag(buf, kk, a, b);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
+                    const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
+                    const T st = kk == s * CL ? from[i][j] : to[i][j];
+                    to[i][j] = tjoin<SR, T>(tjoin<SR, T>(st, p0), p1);
+                }
+        }
+        if constexpr (ARGMAX) {
+            int32_t cv;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(cv) : "s"(int32_t(t * (BK / CL) + s)));
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; j += 4)
+                    record4<SR, T>(ch[i][j], ch[i][j + 1], ch[i][j + 2], ch[i][j + 3], to[i][j],
+                                   to[i][j + 1], to[i][j + 2], to[i][j + 3], from[i][j],
+                                   from[i][j + 1], from[i][j + 2], from[i][j + 3], cv);
+        }
     };
 
     // k-tiles [t0, t1) of this slice; t (and so every chunk index) is global.
@@ -321,51 +435,22 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             patch_tail(buf, kv);
             __syncthreads();
         }
-
-        // The LDS tile holds BK / CL argmax chunks of CL consecutive k.  Each
-        // chunk folds its products into a max3/min3 chain that starts from
-        // the running value, so the running value needs no separate update;
-        // with argmax the chunk is recorded iff the chain's result beats the
-        // value held before the chunk strictly (the reference's "keep acc iff
-        // acc >= p").
+        asm volatile("" : "+v"(swz_t));
+        if constexpr (ARGMAX) {
 #pragma unroll
-        for (int s = 0; s < BK / CL; ++s) {
-            T an[TM][TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) an[i][j] = acc[i][j];
-#pragma unroll
-            for (int kk = s * CL; kk < (s + 1) * CL; kk += 2) {
-                T a[TM][2], b[2][TN];
-                load_frag(buf, kk, a, b);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
-                        const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
-                        an[i][j] = tjoin<SR, T>(tjoin<SR, T>(an[i][j], p0), p1);
-                    }
+            for (int s = 0; s < BK / CL; s += 2) {
+                chunk(t, buf, s, acc, alt);
+                chunk(t, buf, s + 1, alt, acc);
             }
+        } else {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    if constexpr (ARGMAX) {
-                        if (tbetter<SR, T>(an[i][j], acc[i][j]))
-                            ch[i][j] = int32_t(t * (BK / CL) + s);
-                    }
-                    acc[i][j] = an[i][j];
-                }
+            for (int s = 0; s < BK / CL; ++s) chunk(t, buf, s, acc, acc);
         }
     }
 
     // ---- epilogue ------------------------------------------------------------
-    // Output (i, j) of this thread: tile row ty*4+i, tile column (j>>2)*64 +
-    // tx*4 + (j&3); its local id is row*BN + column.
     auto store_row = [&](int i, const T (&v)[TN], const int32_t (&ix)[TN]) {
-        const int64_t gr = row0 + ty * 4 + i;
+        const int64_t gr = row0 + trow(i);
         if (gr >= M) return;
 #pragma unroll
         for (int g = 0; g < TN / 4; ++g) {
@@ -383,138 +468,140 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             }
         }
     };
+    // An output whose chain met a NaN product ends NaN (f32 chains propagate
+    // NaN).  Unsplit, it is recomputed after the stores with the reference's
+    // serial rule over the whole k range (cpu_select: B read down its column,
+    // or B^T along its row) and stored again; a split-K slice leaves NaN in
+    // its partial and tg_merge_splits recomputes the output.  Rare: only NaN
+    // inputs, or infinities meeting (-inf + inf, 0 * inf), make NaN products.
+    // The outputs to redo go through a bit mask and one runtime loop, so the
+    // serial code is not unrolled per output and does not press on the main
+    // loop's registers.
+    const bool split = gridDim.y > 1;
+    static_assert(TM * TN <= 64, "one mask bit per output");
+    uint64_t redo = 0;
+    auto redo_outputs = [&](bool argmax_out) {
+#pragma unroll 1
+        while (redo) {
+            const int o = __builtin_ctzll(redo);
+            redo &= redo - 1;
+            const int64_t gr = row0 + trow(o / TN), gc = col0 + tcol(o % TN);
+            if (split || gr >= M || gc >= N) continue;
+            T v;
+            int32_t ix;
+            if (argmax_out)
+                cpu_select<SR, T>(A + gr * K, 1, BT + gc * K, 1, K, v, ix);
+            else
+                cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
+            C[gr * N + gc] = v;
+            if (argmax_out) IDX[gr * N + gc] = ix;
+        }
+    };
     if constexpr (!ARGMAX) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             int32_t none[TN] = {};
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                if (tisnan(acc[i][j])) redo |= uint64_t(1) << (i * TN + j);
             store_row(i, acc[i], none);
         }
+        if constexpr (std::is_floating_point<T>::value) redo_outputs(false);
     } else {
         // Exact first k inside each output's recorded chunk c.  The window of
         // chunk c holds the final value as its own maximum (no product of an
         // earlier chunk reaches it), so the window alone gives the target and
-        // the first k attaining it.  Outputs are resolved in chunk order
-        // (LDS counting sort), so workgroups running side by side read the
-        // same A-row / B^T-row segments at about the same time and mostly hit
-        // in cache.  The resolve returns the offset inside the chunk and, for
-        // a zero maximum, the sign of the first zero product (the CPU keeps
-        // the first occurrence's bits).
+        // the first k attaining it.  Outputs are resolved in chunk order (LDS
+        // counting sort), so workgroups running side by side read the same
+        // A-row / B^T-row segments at about the same time and mostly hit in
+        // cache.  The resolve returns the offset inside the chunk and, for a
+        // zero maximum, the sign of the first zero product (the CPU keeps the
+        // first occurrence's bits); it writes them over the output's chunk
+        // slot, and the thread that owns the output combines them with its
+        // own record.
         constexpr uint16_t NONE = 0xFFFF;
         uint32_t* hist = reinterpret_cast<uint32_t*>(dl_lds + Cfg::HIST_OFF);
         uint16_t* chs = reinterpret_cast<uint16_t*>(dl_lds + Cfg::CHS_OFF);
         uint16_t* list = reinterpret_cast<uint16_t*>(dl_lds + Cfg::LIST_OFF);
-        uint8_t* res = dl_lds + Cfg::RES_OFF;
         int* misc = reinterpret_cast<int*>(dl_lds + Cfg::MISC_OFF);
-        // Buckets: chunk >> shift, at most NB_MAX of them.
+        static_assert(Cfg::MISC_OFF + 64 <= Cfg::LDS_BYTES, "epilogue arrays fit the LDS block");
+        static_assert(Cfg::NB <= TG_THREADS, "one bucket per thread in the scan");
+        // Buckets: chunk >> shift, at most NB of them.
         const int64_t nchunks = (K + CL - 1) / CL;
         int shift = 0;
-        while (((nchunks - 1) >> shift) >= Cfg::NB_MAX) ++shift;
+        while (((nchunks - 1) >> shift) >= Cfg::NB) ++shift;
         const int nb = int(((nchunks - 1) >> shift) + 1);
 
-        __syncthreads();  // every wave is done with the tile buffers
-        for (int b = tid; b < nb; b += TG_THREADS) hist[b] = 0;
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
-                chs[lid] = ch[i][j] < 0 ? NONE : uint16_t(ch[i][j]);
-            }
-        __syncthreads();
-        uint16_t rank[TM][TN];
+        // NaN chains: no record is meaningful; -2 keeps them out of the sort.
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                rank[i][j] = ch[i][j] < 0 ? 0 : uint16_t(atomicAdd(&hist[ch[i][j] >> shift], 1u));
-        __syncthreads();
-        // Exclusive scan of the bucket counts, 8 buckets per thread.
-        constexpr int PER = Cfg::NB_MAX / TG_THREADS;
-        int cnt[PER];
-        int mine = 0;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int b = tid * PER + q;
-            cnt[q] = b < nb ? int(hist[b]) : 0;
-            mine += cnt[q];
-        }
-        int total = 0;
-        int run = block_exclusive_scan(mine, misc, total);
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int b = tid * PER + q;
-            if (b < nb) hist[b] = uint32_t(run);
-            run += cnt[q];
-        }
+                if (tisnan(acc[i][j])) ch[i][j] = -2;
+        __syncthreads();  // every wave is done with the tile buffers
+        if (tid < Cfg::NB) hist[tid] = 0;
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                if (ch[i][j] >= 0) {
-                    const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
-                    list[hist[ch[i][j] >> shift] + rank[i][j]] = uint16_t(lid);
-                }
+                const int lid = trow(i) * BN + tcol(j);
+                chs[lid] = ch[i][j] < 0 ? NONE : uint16_t(ch[i][j]);
+                if (ch[i][j] >= 0) atomicAdd(&hist[ch[i][j] >> shift], 1u);
             }
         __syncthreads();
+        // Exclusive scan of the bucket counts; the starts become cursors.
+        const int cnt = tid < nb ? int(hist[tid]) : 0;
+        int total = 0;
+        const int start = block_exclusive_scan(cnt, misc, total);
+        if (tid < nb) hist[tid] = uint32_t(start);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                if (ch[i][j] >= 0)
+                    list[atomicAdd(&hist[ch[i][j] >> shift], 1u)] = uint16_t(trow(i) * BN + tcol(j));
+        __syncthreads();
 
-        // Resolve, chunk-sorted, one output per thread at a time (two in
-        // flight would push the kernel past the 3-waves-per-SIMD register
-        // budget of the main loop).
+        // Resolve, chunk-sorted, one output per thread at a time.
         constexpr int NW = CL / 4;
-        constexpr int G = 1;
-        for (int e0 = 0; e0 < total; e0 += TG_THREADS * G) {
-            int lid[G];
-            int64_t c[G];
-            bool valid[G];
-            Vec16<T> av[G][NW], bv[G][NW];
-            const T* ap[G];
-            const T* bp[G];
+        for (int e = tid; e < total; e += TG_THREADS) {
+            const int lid = int(list[e]);
+            const int64_t c = int64_t(chs[lid]);
+            // Clamped like the tile loads (outputs past M or N are not
+            // stored; their windows just stay in bounds).  Quads of a window
+            // past K read the row's last quad: duplicates that come after
+            // their originals, so the first match is a k < K.
+            const int64_t gr = row0 + lid / BN, gc = col0 + (lid & (BN - 1));
+            const T* ap = A + (gr < M ? gr : M - 1) * K + c * CL;
+            const T* bp = BT + (gc < N ? gc : N - 1) * K + c * CL;
+            T p[CL];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const int e = e0 + g * TG_THREADS + tid;
-                valid[g] = e < total;
-                lid[g] = valid[g] ? int(list[e]) : 0;
-                c[g] = valid[g] ? int64_t(chs[lid[g]]) : 0;
-                // Clamped like the tile loads (outputs past M or N are not
-                // stored; their windows just stay in bounds).  Quads of a
-                // window past K read the row's last quad: duplicates that
-                // come after their originals, so the first match is a k < K.
-                const int64_t gr = row0 + lid[g] / BN, gc = col0 + (lid[g] & (BN - 1));
-                ap[g] = A + (gr < M ? gr : M - 1) * K + c[g] * CL;
-                bp[g] = BT + (gc < N ? gc : N - 1) * K + c[g] * CL;
+            for (int w = 0; w < NW; ++w) {
+                const int64_t off = (!TAILK || c * CL + w * 4 <= K - 4) ? w * 4 : K - 4 - c * CL;
+                const Vec16<T> av = *reinterpret_cast<const Vec16<T>*>(ap + off);
+                const Vec16<T> bv = *reinterpret_cast<const Vec16<T>*>(bp + off);
 #pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    const int64_t off =
-                        (!TAILK || c[g] * CL + w * 4 <= K - 4) ? w * 4 : K - 4 - c[g] * CL;
-                    av[g][w] = *reinterpret_cast<const Vec16<T>*>(ap[g] + off);
-                    bv[g][w] = *reinterpret_cast<const Vec16<T>*>(bp[g] + off);
-                }
+                for (int q = 0; q < 4; ++q) p[w * 4 + q] = tmul<SR, T>(av.v[q], bv.v[q]);
             }
+            T mx = tjoin<SR, T>(p[0], p[1]);
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                T p[CL];
+            for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
+            // Last match scanning downwards == first match; groups of 8
+            // compares keep few lane masks live at once.
+            int f = 0;
 #pragma unroll
-                for (int kk = 0; kk < CL; ++kk)
-                    p[kk] = tmul<SR, T>(av[g][kk >> 2].v[kk & 3], bv[g][kk >> 2].v[kk & 3]);
-                T mx = tjoin<SR, T>(p[0], p[1]);
+            for (int q = CL / 8 - 1; q >= 0; --q) {
 #pragma unroll
-                for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
-                // Last match scanning downwards == first match; groups of 8
-                // compares keep few lane masks live at once.
-                int f = 0;
-#pragma unroll
-                for (int q = CL / 8 - 1; q >= 0; --q) {
-#pragma unroll
-                    for (int kk = q * 8 + 7; kk >= q * 8; --kk) f = (p[kk] == mx) ? kk : f;
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                int r = f;
-                if constexpr (std::is_floating_point<T>::value) {
-                    if (mx == T(0) && __builtin_signbit(tmul<SR, T>(ap[g][f], bp[g][f]))) r |= 32;
-                }
-                if (valid[g]) res[lid[g]] = uint8_t(r);
+                for (int kk = q * 8 + 7; kk >= q * 8; --kk) f = (p[kk] == mx) ? kk : f;
+                __builtin_amdgcn_sched_barrier(0);
             }
+            int r = f;
+            if constexpr (std::is_floating_point<T>::value) {
+                if (mx == T(0) && __builtin_signbit(tmul<SR, T>(ap[f], bp[f]))) r |= 32;
+            }
+            chs[lid] = uint16_t(r);
         }
         __syncthreads();
 
@@ -524,14 +611,16 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             int32_t ix[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int lid = (ty * 4 + i) * BN + (j >> 2) * 64 + tx * 4 + (j & 3);
-                const uint16_t cc = chs[lid];
-                if (cc == NONE) {  // the tropical zero was never beaten
+                if (ch[i][j] == -2) {  // the chain met a NaN product: redone below
+                    v[j] = acc[i][j];
+                    ix[j] = 0;
+                    redo |= uint64_t(1) << (i * TN + j);
+                } else if (ch[i][j] < 0) {  // the tropical zero was never beaten
                     v[j] = tzero<SR, T>();
                     ix[j] = 0;
                 } else {
-                    const int r = res[lid];
-                    ix[j] = int32_t(cc) * CL + (r & 31);
+                    const int r = chs[trow(i) * BN + tcol(j)];
+                    ix[j] = ch[i][j] * CL + (r & 31);
                     v[j] = acc[i][j];
                     if constexpr (std::is_floating_point<T>::value) {
                         if (v[j] == T(0)) v[j] = (r & 32) ? -T(0) : T(0);
@@ -540,6 +629,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             }
             store_row(i, v, ix);
         }
+        if constexpr (std::is_floating_point<T>::value) redo_outputs(true);
     }
 }
 

@@ -147,7 +147,9 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
-    auto below = [](int32_t x, int bits) { return uint32_t(x + (1 << (bits - 1))) < (1u << bits); };
+    auto below = [](int32_t x, int bits) {
+        return uint32_t(x) + (1u << (bits - 1)) < (1u << bits);  // unsigned: no overflow
+    };
     // Rewrites B in LDS into keys: b*256 + (255 - k) (MinPlus: + k); ends
     // with a barrier.
     auto rewrite_b = [&](int form) {
@@ -393,6 +395,26 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                 if constexpr (!std::is_floating_point<T>::value) v = acc[i][j];
                 cv.v[j] = c < 0 ? tzero<SR, T>() : v;
                 iv.v[j] = c < 0 ? 0 : k0 + f;
+                if constexpr (std::is_floating_point<T>::value) {
+                    if (tisnan(acc[i][j])) {
+                        // The chain met a NaN product: the reference's serial
+                        // rule over the whole (LDS-resident) k range.
+                        T x = tzero<SR, T>();
+                        int32_t ix = 0;
+                        for (int k = 0; k < KT * BK; ++k) {
+                            const int tt = k / BK, q = k % BK;
+                            const T ak = As[tt * Cfg::A_TILE + row * BK + (((q >> 2) ^ swz) << 2) + (q & 3)];
+                            const T bk = Bs[tt * Cfg::B_TILE + q * BN + tx * 4 + j];
+                            const T pk = tmul<SR, T>(ak, bk);
+                            if (ttake<SR, T>(pk, x)) {
+                                x = pk;
+                                ix = k;
+                            }
+                        }
+                        cv.v[j] = x;
+                        iv.v[j] = ix;
+                    }
+                }
             }
             store_row(i, cv, iv);
         }

@@ -156,7 +156,9 @@ tg_gemm_kres8(const int32_t* __restrict__ A, const int32_t* __restrict__ B,
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     };
-    auto below = [](int32_t x, int bits) { return uint32_t(x + (1 << (bits - 1))) < (1u << bits); };
+    auto below = [](int32_t x, int bits) {
+        return uint32_t(x) + (1u << (bits - 1)) < (1u << bits);  // unsigned: no overflow
+    };
     // Workgroup-wide AND of pred, voted through four flag words in ring slot
     // 1 (two barriers; the leading one also ends every earlier use of the
     // ring).  Slot 1 is next written after the barrier that follows the

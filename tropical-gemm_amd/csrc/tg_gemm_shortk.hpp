@@ -15,11 +15,14 @@
 //     (B is K x N, small at short K, and re-read by every wave).
 //   * No LDS and at most 128 VGPRs (f32 argmax: 124), so 4 waves per SIMD
 //     keep the products of some waves in flight while others store.
-// ARGMAX: every product in k order updates (value, k) on a strict
-// improvement, which keeps the first k attaining the optimum (the
-// reference's tie rule, core/argmax.rs:24-33 and core/kernel.rs:119-167);
-// outputs that never beat the tropical zero keep it with argmax 0.
-// Value-only: max3/min3 chains from the tropical zero.
+// ARGMAX: every product in k order updates (value, k) under the reference's
+// select rule (ttake: strict improvement for non-NaN values, which keeps the
+// first k attaining the optimum, core/argmax.rs:24-33 and
+// core/kernel.rs:119-167; a NaN product replaces, as on the CPU); outputs
+// that never beat the tropical zero keep it with argmax 0.
+// Value-only: max3/min3 chains from the tropical zero (f32: NaN-propagating,
+// with the serial rule for outputs that end NaN; f64: the select rule per
+// product, since v_max_f64 drops NaN).
 //
 // Host-checked requirements: N % 4 == 0, B, C (and IDX) 16-byte aligned with
 // batch strides sB, sC multiples of 4; any M >= 1, K >= 1.
@@ -109,12 +112,18 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
                 for (int j = 0; j < 4; ++j) p[j] = tmul<SR, T>(a[r][kk], b[kk][j]);
                 if constexpr (ARGMAX) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) better[j] = tbetter<SR, T>(p[j], acc[r][j]);
+                    for (int j = 0; j < 4; ++j) better[j] = ttake<SR, T>(p[j], acc[r][j]);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         acc[r][j] = better[j] ? p[j] : acc[r][j];
                         ix[r][j] = better[j] ? kg : ix[r][j];
                     }
+                } else if constexpr (std::is_same<T, double>::value) {
+                    // v_max_f64 would drop a NaN product: the select rule.
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) better[j] = ttake<SR, T>(p[j], acc[r][j]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[r][j] = better[j] ? p[j] : acc[r][j];
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) acc[r][j] = tjoin<SR, T>(acc[r][j], p[j]);
@@ -127,6 +136,18 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
     for (; k0 < K; ++k0) block(k0, std::integral_constant<int, 1>());
 
     if (!col_ok) return;
+    if constexpr (!ARGMAX && std::is_same<T, float>::value) {
+        // An f32 value chain that met a NaN product ends NaN: recompute it
+        // with the reference's serial rule (K is short here).
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (tisnan(acc[r][j]) && r0 + r < M) {
+                    int32_t unused;
+                    cpu_select<SR, T>(A + (r0 + r) * K, 1, B + col + j, N, K, acc[r][j], unused);
+                }
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (r0 + r >= M) break;

@@ -5,11 +5,9 @@
 //                      (TROPICAL_GEMM_{F32,F64,I32,I64} 86-520,
 //                       TROPICAL_GEMM_ARGMAX_* 526-996, batched 1094-1219)
 //   tg_transpose       B -> B^T staging for the argmax epilogue (new)
-//   tg_backward_rows   grad_A scatter (TROPICAL_BACKWARD_A 1002-1018)
-//   tg_backward_cols_lds  grad_B scatter into LDS column blocks
-//                      (TROPICAL_BACKWARD_B 1020-1036)
-//   tg_backward_cols   grad_B fallback with global atomics (huge K)
 //   tg_fill_zero       zero fill used instead of hipMemsetAsync
+// The backward scatters (TROPICAL_BACKWARD_A/B 1002-1036) are in
+// tg_backward.hpp.
 //
 // All matrices are row-major here; the host layer maps column-major calls
 // onto row-major ones with the operand swap C^T = B^T (x) A^T
@@ -137,6 +135,25 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     }
 
     // ---- global -> register staging ------------------------------------
+    // f64 chains use v_max_f64 / v_min_f64, which drop NaN operands, so a
+    // NaN product would vanish from a chain.  NaN products come only from NaN
+    // operands or from infinities meeting (+inf + -inf; 0 * inf for MaxMul):
+    // the loads classify every in-bounds operand (one v_cmp_class each into
+    // wave masks), and a tile whose operands could make a NaN product is
+    // recomputed with the reference's serial rule in the epilogue.
+    constexpr bool CHECK = std::is_same<T, double>::value && !EXACT;
+    constexpr int CLS1 = SR == SR_MAXMUL ? 516 : 512;  // +-inf | +inf
+    constexpr int CLS2 = SR == SR_MAXMUL ? 96 : 4;     // +-0   | -inf
+    uint64_t fl[6] = {0, 0, 0, 0, 0, 0};  // A: nan, c1, c2; B: nan, c1, c2
+    __shared__ int danger_flags;
+    if (CHECK && tid == 0) danger_flags = 0;
+    auto classify = [&](bool inb, T x, int o) {
+        if constexpr (CHECK) {
+            fl[o] |= __ballot(inb && __builtin_amdgcn_class(x, 3));
+            fl[o + 1] |= __ballot(inb && __builtin_amdgcn_class(x, CLS1));
+            fl[o + 2] |= __ballot(inb && __builtin_amdgcn_class(x, CLS2));
+        }
+    };
     Vec16<T> ra[NVA], rb[NVB];
     auto load_tiles = [&](int64_t k0) {
 #pragma unroll
@@ -158,6 +175,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                 for (int e = 0; e < VW; ++e)
                     ra[v].v[e] = (gr < M && gk + e < K) ? A[gr * K + gk + e] : T(0);
             }
+#pragma unroll
+            for (int e = 0; e < VW; ++e) classify(gr < M && gk + e < K, ra[v].v[e], 0);
         }
 #pragma unroll
         for (int v = 0; v < NVB; ++v) {
@@ -178,6 +197,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                 for (int e = 0; e < VW; ++e)
                     rb[v].v[e] = (gk < K && gc + e < N) ? B[gk * N + gc + e] : T(0);
             }
+#pragma unroll
+            for (int e = 0; e < VW; ++e) classify(gk < K && gc + e < N, rb[v].v[e], 3);
         }
     };
     auto store_tiles = [&](int buf) {
@@ -238,7 +259,9 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         if (t + 1 < ntiles) load_tiles(k0 + BK);
 
         if constexpr (EXACT) {
-            // Every product in k order; strict improvement keeps the first k.
+            // Every product in k order under the reference's select rule
+            // (ttake: strict improvement for non-NaN values, so the first k
+            // is kept; a NaN product replaces, as on the CPU).
             auto step = [&](int kk) {
                 T a0[TM], b0[TN];
                 load_frag(buf, kk, a0, b0);
@@ -256,7 +279,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
 #pragma unroll
                         for (int j = 0; j < TN; ++j) {
                             p[j] = tmul<SR, T>(a0[i], b0[j]);
-                            better[j] = tbetter<SR, T>(p[j], acc[i][j]);
+                            better[j] = ttake<SR, T>(p[j], acc[i][j]);
                         }
 #pragma unroll
                         for (int j = 0; j < TN; ++j) {
@@ -270,7 +293,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
 #pragma unroll
                         for (int j = 0; j < TN; ++j) {
                             const T p = tmul<SR, T>(a0[i], b0[j]);
-                            const bool better = tbetter<SR, T>(p, acc[i][j]);
+                            const bool better = ttake<SR, T>(p, acc[i][j]);
                             acc[i][j] = better ? p : acc[i][j];
                             ch[i][j] = better ? kg : ch[i][j];
                         }
@@ -344,7 +367,38 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     }
 
     // ---- epilogue ------------------------------------------------------------
+    // Outputs computed with the reference's serial rule instead of the fast
+    // chain: f32 chains that met a NaN product (they end NaN), and every
+    // output of an f64 tile whose operands could make one (CHECK above).
+    bool danger = false;
+    if constexpr (CHECK) {
+        const int w = (fl[0] != 0) | (fl[1] != 0) << 1 | (fl[2] != 0) << 2 | (fl[3] != 0) << 3 |
+                      (fl[4] != 0) << 4 | (fl[5] != 0) << 5;
+        if ((tid & 63) == 0 && w != 0) atomicOr(&danger_flags, w);
+        __syncthreads();
+        const int f = danger_flags;
+        danger = (f & 1) || (f & 8) || ((f & 2) && (f & 32)) || ((f & 4) && (f & 16));
+    }
+    auto exact = [&](int64_t gr, int64_t gc, T& v, int32_t& ix) {
+        if constexpr (ARGMAX && !EXACT)
+            cpu_select<SR, T>(A + gr * K, 1, BT + gc * K, 1, K, v, ix);
+        else
+            cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
+    };
     if constexpr (!ARGMAX || EXACT) {
+        if constexpr (!EXACT) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+                    const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
+                    if ((danger || tisnan(acc[i][j])) && gr < M && gc < N) {
+                        int32_t ix;
+                        exact(gr, gc, acc[i][j], ix);
+                    }
+                }
+        }
         // Values (and EXACT indices) as they stand.  Each thread's columns
         // come in groups of 4 consecutive ones: one 16-byte store per group
         // and array when the rows are 16-byte aligned, element stores at the
@@ -490,6 +544,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                         idx[g] = 0;
                     }
                     if (gr < M && gc[g] < N) {
+                        if (danger || tisnan(acc[i][j0 + g])) exact(gr, gc[g], val[g], idx[g]);
                         C[gr * N + gc[g]] = val[g];
                         IDX[gr * N + gc[g]] = idx[g];
                     }
@@ -537,215 +592,6 @@ __global__ __launch_bounds__(256) void tg_fill_zero(unsigned char* __restrict__ 
         reinterpret_cast<uint4*>(p)[v] = make_uint4(0u, 0u, 0u, 0u);
     const int64_t tail0 = nvec * 16;
     for (int64_t b = tail0 + int64_t(blockIdx.x) * 256 + threadIdx.x; b < bytes; b += stride) p[b] = 0;
-}
-
-// ---------------------------------------------------------------------------
-// Floating-point add into LDS.  On gfx950 ds_add_f32 takes about three
-// clocks per distinct address in a wave (measured: 0.33 lane-updates per
-// clock and CU with scattered bins) but merges lanes that share an address,
-// while a compare-and-swap of the bits runs at ~2.4 when bins rarely collide
-// and costs more than the hardware add when most lanes share a few bins.  So
-// with cas = true f32 tries ROUNDS CAS and the lanes whose CAS lost every
-// race (another lane or wave changed the bin first) fall back to the hardware
-// add;
-// callers pass cas = false for waves whose indices repeat a lot
-// (repetitive_wave).  Either way the sum is the same set of IEEE additions in
-// some order, as with the plain atomic.  f64 always uses ds_add_f64, which
-// showed no such penalty.
-// ---------------------------------------------------------------------------
-template <int ROUNDS, typename T>
-__device__ __forceinline__ void lds_add(T* p, T v, bool cas) {
-    if constexpr (sizeof(T) == 4) {
-        if (cas) {
-            uint32_t* q = reinterpret_cast<uint32_t*>(p);
-            uint32_t old = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-            for (int r = 0; r < ROUNDS; ++r) {
-                const uint32_t prev = atomicCAS(q, old, __float_as_uint(__uint_as_float(old) + v));
-                if (prev == old) return;
-                old = prev;
-            }
-        }
-    }
-    atomicAdd(p, v);
-}
-
-// True when more than 1/8 of the wave's lanes share their index with lane ^ 1
-// or lane ^ 2 (a few bins take most of the wave: the argmax of a row often
-// repeats, one distinct index per 64 lanes in the worst case).  Every lane
-// calls it (all lanes hold a defined index).
-__device__ __forceinline__ bool repetitive_wave(int32_t k) {
-    // DPP quad permutations [1,0,3,2] and [2,3,0,1] (VALU, no LDS traffic).
-    const int32_t k1 = __builtin_amdgcn_update_dpp(k, k, 0xB1, 0xF, 0xF, true);
-    const int32_t k2 = __builtin_amdgcn_update_dpp(k, k, 0x4E, 0xF, 0xF, true);
-    return __popcll(__ballot(k == k1)) + __popcll(__ballot(k == k2)) > 16;
-}
-
-// ---------------------------------------------------------------------------
-// grad_A rows: one workgroup per (row i, batch z); the row of grad_A (K
-// values) is accumulated in LDS (lds_add) and written out whole, so no
-// global atomics and no separate zero fill are needed.
-//   MULT=true: MaxMul rule, g *= B[kk, j]  (OTHER = B, row-major K x N).
-// grid = (M, 1, batch), block = 256, dynamic LDS = K * sizeof(T).
-// ---------------------------------------------------------------------------
-template <typename T, bool MULT>
-__global__ __launch_bounds__(256) void tg_backward_rows(const T* __restrict__ G,
-                                                        const int32_t* __restrict__ IDX,
-                                                        const T* __restrict__ OTHER,
-                                                        T* __restrict__ GA, int64_t M, int64_t N,
-                                                        int64_t K, int64_t sC, int64_t sO,
-                                                        int64_t sA) {
-    extern __shared__ __align__(16) unsigned char lds_raw[];
-    T* row = reinterpret_cast<T*>(lds_raw);
-    const int64_t i = blockIdx.x;
-    const int64_t z = blockIdx.z;
-    G += z * sC;
-    IDX += z * sC;
-    GA += z * sA;
-    if (MULT) OTHER += z * sO;
-    for (int64_t k = threadIdx.x; k < K; k += 256) row[k] = T(0);
-    __syncthreads();
-    // U entries per thread per pass, all loads issued before the LDS adds.
-    constexpr int U = 8;
-    for (int64_t j0 = 0; j0 < N; j0 += 256 * U) {
-        int32_t kk[U];
-        T g[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t j = j0 + u * 256 + threadIdx.x;
-            kk[u] = j < N ? IDX[i * N + j] : -1;
-            g[u] = j < N ? G[i * N + j] : T(0);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const bool cas = !repetitive_wave(kk[u]);
-            if (kk[u] >= 0 && int64_t(kk[u]) < K) {
-                T v = g[u];
-                if (MULT) v = v * OTHER[int64_t(kk[u]) * N + j0 + u * 256 + threadIdx.x];
-                // Two rounds: a row's argmax often pairs up within a wave
-                // (measured 6% faster on C5's argmax than one round).
-                lds_add<2>(&row[kk[u]], v, cas);
-            }
-        }
-    }
-    __syncthreads();
-    for (int64_t k = threadIdx.x; k < K; k += 256) GA[i * K + k] = row[k];
-}
-
-// grad_A fallback for rows that do not fit in LDS: global atomics into a
-// zero-filled grad_A.  grid = (ceil(M*N/256), 1, batch).
-template <typename T, bool MULT>
-__global__ __launch_bounds__(256) void tg_backward_rows_global(const T* __restrict__ G,
-                                                               const int32_t* __restrict__ IDX,
-                                                               const T* __restrict__ OTHER,
-                                                               T* __restrict__ GA, int64_t M,
-                                                               int64_t N, int64_t K, int64_t sC,
-                                                               int64_t sO, int64_t sA) {
-    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (o >= M * N) return;
-    const int64_t z = blockIdx.z;
-    G += z * sC;
-    IDX += z * sC;
-    GA += z * sA;
-    if (MULT) OTHER += z * sO;
-    const int64_t i = o / N, j = o - (o / N) * N;
-    const int32_t kk = IDX[o];
-    if (kk >= 0 && int64_t(kk) < K) {
-        T g = G[o];
-        if (MULT) g = g * OTHER[int64_t(kk) * N + j];
-        unsafeAtomicAdd(&GA[i * K + kk], g);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// grad_B: global atomics into a zero-filled grad_B (K x N).
-//   MULT=true: MaxMul rule, g *= A[i, kk]  (OTHER = A, row-major M x K).
-// grid = (ceil(M*N/256), 1, batch).
-// ---------------------------------------------------------------------------
-template <typename T, bool MULT>
-__global__ __launch_bounds__(256) void tg_backward_cols(const T* __restrict__ G,
-                                                        const int32_t* __restrict__ IDX,
-                                                        const T* __restrict__ OTHER,
-                                                        T* __restrict__ GB, int64_t M, int64_t N,
-                                                        int64_t K, int64_t sC, int64_t sO,
-                                                        int64_t sB) {
-    const int64_t o = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (o >= M * N) return;
-    const int64_t z = blockIdx.z;
-    G += z * sC;
-    IDX += z * sC;
-    GB += z * sB;
-    if (MULT) OTHER += z * sO;
-    const int64_t i = o / N, j = o - (o / N) * N;
-    const int32_t kk = IDX[o];
-    if (kk >= 0 && int64_t(kk) < K) {
-        T g = G[o];
-        if (MULT) g = g * OTHER[i * K + kk];
-        unsafeAtomicAdd(&GB[int64_t(kk) * N + j], g);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// grad_B for a block of BJ = 2^bj_log2 consecutive columns, accumulated in
-// LDS (K x BJ values, at most LDS_ELEMS) and written out whole: no global
-// atomics and no separate zero fill.  Consecutive column blocks share cache
-// lines, so the block order is remapped to keep neighbours on one XCD.
-//   MULT=true: MaxMul rule, g *= A[i, kk]  (OTHER = A, row-major M x K).
-// grid = (ceil(N / BJ), 1, batch), block = 512.
-// ---------------------------------------------------------------------------
-template <typename T, bool MULT, int LDS_ELEMS>
-__global__ __launch_bounds__(512) void tg_backward_cols_lds(const T* __restrict__ G,
-                                                            const int32_t* __restrict__ IDX,
-                                                            const T* __restrict__ OTHER,
-                                                            T* __restrict__ GB, int64_t M, int64_t N,
-                                                            int64_t K, int64_t sC, int64_t sO,
-                                                            int64_t sB, int bj_log2) {
-    __shared__ T acc[LDS_ELEMS];
-    const int BJ = 1 << bj_log2;
-    const int nblocks = int(gridDim.x);
-    int bid = int(blockIdx.x);
-    if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-    const int64_t j0 = int64_t(bid) * BJ;
-    const int64_t z = blockIdx.z;
-    G += z * sC;
-    IDX += z * sC;
-    GB += z * sB;
-    if (MULT) OTHER += z * sO;
-    const int64_t total = K * BJ;
-    for (int64_t e = threadIdx.x; e < total; e += 512) acc[e] = T(0);
-    __syncthreads();
-    // Entries (i, c), c fastest: consecutive lanes read consecutive columns.
-    constexpr int U = 8;
-    const int64_t ne = M * BJ;
-    for (int64_t e0 = 0; e0 < ne; e0 += 512 * U) {
-        int32_t kk[U];
-        T g[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t e = e0 + u * 512 + threadIdx.x;
-            const int64_t i = e >> bj_log2;
-            const int64_t j = j0 + (e & (BJ - 1));
-            const bool ok = e < ne && j < N;
-            kk[u] = ok ? IDX[i * N + j] : -1;
-            g[u] = ok ? G[i * N + j] : T(0);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (kk[u] >= 0 && int64_t(kk[u]) < K) {
-                const int64_t e = e0 + u * 512 + threadIdx.x;
-                T v = g[u];
-                if (MULT) v = v * OTHER[(e >> bj_log2) * K + kk[u]];
-                // Neighbouring lanes hold neighbouring columns, so their
-                // bins differ even where the argmax repeats: always CAS.
-                lds_add<1>(&acc[int64_t(kk[u]) * BJ + (e & (BJ - 1))], v, true);
-            }
-        }
-    }
-    __syncthreads();
-    for (int64_t e = threadIdx.x; e < total; e += 512) {
-        const int64_t j = j0 + (e & (BJ - 1));
-        if (j < N) GB[(e >> bj_log2) * N + j] = acc[e];
-    }
 }
 
 }  // namespace tg

@@ -56,6 +56,9 @@ SIGNATURES = {
     "tg_gemm_workspace_size": ([_i32, _i64, _i64, _i64, _i64, _i32], _sz),
     "tg_gemm_ws": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp],
                    _i32),
+    "tg_gemm_plan": ([_i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                      _i64, _sz], ctypes.c_char_p),
+    "tg_backward_plan": ([_i32, _i32, _i32, _i64, _i64, _i64, _i64], ctypes.c_char_p),
     "tg_gemm_strided_batched": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                  _i64, _i64, _i64, _i64, _vp], _i32),
     "tg_gemm_strided_batched_ws": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
@@ -119,6 +122,21 @@ def load():
             fn.restype = res
         _lib = lib
     return _lib
+
+
+def gemm_plan(semiring: str, dtype: str, m: int, n: int, k: int, with_argmax: bool = True,
+              layout: str = "row", workspace_bytes: int | None = None, batch: int = 1,
+              strides=(0, 0, 0), addresses=(256, 256, 256, 256)) -> str:
+    """Name of the kernel path a product would run on (host logic only; the
+    addresses stand for 16-byte aligned buffers and are never touched).
+    workspace_bytes None: the full workspace, as tg_gemm allocates it."""
+    lib = load()
+    if workspace_bytes is None:
+        workspace_bytes = lib.tg_gemm_workspace_size(DTYPE[dtype], batch, m, n, k, int(with_argmax))
+    a, b, c, i = addresses
+    return lib.tg_gemm_plan(SEMIRING[semiring], DTYPE[dtype], LAYOUT[layout], a, b, c,
+                            i if with_argmax else None, batch, m, n, k, *strides,
+                            workspace_bytes).decode()
 
 
 def last_error() -> str:
