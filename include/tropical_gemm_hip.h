@@ -155,6 +155,23 @@ int tg_gemm_ws(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layou
                int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* tg_gemm that allocates nothing (no hipMalloc / hipFree, no allocating
+ * library call): its workspace is a fixed 64 MiB device array of the library
+ * (TG_NOALLOC_SCRATCH_BYTES), one per device, held until the process ends.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid it).  A
+ * problem whose kernel needs more workspace than that (argmax with
+ * k x max(m, n) elements above it on the chunked-argmax paths) is rejected
+ * with TG_ERR_INVALID_ARGUMENT before any device work.  Every call on one
+ * device shares that device's array, so calls that overlap on one device
+ * (other streams, other host threads) race; serialise them.  The kernels
+ * write every scratch byte they read, so nothing needs clearing between
+ * calls.  Same arguments, results and errors as tg_gemm otherwise. */
+#define TG_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int tg_gemm_noalloc(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                    const void* A, const void* B, void* C, int32_t* argmax,
+                    int64_t m, int64_t n, int64_t k, void* stream);
+
 /*
  * Strided batched product: C[t] = A[t] (x) B[t] for t < batch, element
  * strides between consecutive matrices.  Replaces

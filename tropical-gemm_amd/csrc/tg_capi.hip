@@ -875,6 +875,51 @@ int gemm_impl(int device, tg_semiring sr, tg_dtype dt, tg_layout layout, const v
 }
 
 // ----------------------------------------------------------------------------
+// Workspace without allocation (tg_gemm_noalloc)
+// ----------------------------------------------------------------------------
+
+// The workspace of tg_gemm_noalloc: one fixed array in the code object's
+// zero-initialised device data.  Each device that loads the library holds its
+// own copy from the module's load until the process ends.  On the host the
+// name `scratch` is only a stand-in, never a device address: host code uses
+// the address hipGetSymbolAddress returns for the current device
+// (scratch_address), in kernel arguments as everywhere else.
+constexpr size_t kScratchBytes = TG_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+// Device address of `scratch` on `device`, which must be the current device.
+// Looked up once per device (tg_context_init, or the first tg_gemm_noalloc
+// call on that device) and kept.
+int scratch_address(int device, void** out) {
+    if (device < 0 || device >= kScratchMaxDevices)
+        return fail(TG_ERR_INVALID_ARGUMENT,
+                    "tg_gemm_noalloc supports devices 0.." + std::to_string(kScratchMaxDevices - 1));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (ptr == nullptr) return fail(TG_ERR_DRIVER, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return TG_OK;
+}
+
+// Scratch bytes the planned path reads (0 when it reads none).  The plan is
+// made with kScratchBytes as the workspace, so split K is only chosen when
+// its partials fit; B^T staging alone may still exceed it.
+size_t scratch_need(tg_dtype dt, const Problem& p, const Plan& pl) {
+    const bool argmax = p.IDX != nullptr;
+    if (!uses_workspace(pl, argmax)) return 0;
+    return ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, pl.splits).total;
+}
+
+// ----------------------------------------------------------------------------
 // Backward
 // ----------------------------------------------------------------------------
 
@@ -1092,6 +1137,11 @@ int tg_context_init(int device) {
     int rc = select_device(device);
     if (rc != TG_OK) return rc;
     TG_HIP(hipFree(nullptr));  // forces runtime/context initialisation
+    if (device < kScratchMaxDevices) {  // tg_gemm_noalloc's workspace address
+        void* unused = nullptr;
+        rc = scratch_address(device, &unused);
+        if (rc != TG_OK) return rc;
+    }
     return TG_OK;
 }
 
@@ -1206,6 +1256,31 @@ int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout, 
             void* stream) {
     return gemm_impl(device, semiring, dtype, layout, A, B, C, argmax, 1, m, n, k, 0, 0, 0, false,
                      nullptr, 0, false, stream);
+}
+
+int tg_gemm_noalloc(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                    const void* A, const void* B, void* C, int32_t* argmax, int64_t m, int64_t n,
+                    int64_t k, void* stream) {
+    int rc = validate_forward(semiring, dtype, layout, A, B, C, 1, m, n, k, 0, 0, 0, false);
+    if (rc != TG_OK) return rc;
+    const Problem p = make_problem(layout, A, B, C, argmax, 1, m, n, k, 0, 0, 0, false);
+    // Host-only planning first, so an oversized problem is rejected before
+    // any device work.
+    const bool empty = m == 0 || n == 0;
+    const Plan pl = empty ? Plan{} : plan_gemm(semiring, dtype, p, kScratchBytes);
+    const size_t need = empty ? 0 : scratch_need(dtype, p, pl);
+    if (need > kScratchBytes)
+        return fail(TG_ERR_INVALID_ARGUMENT,
+                    "tg_gemm_noalloc: this problem needs " + std::to_string(need) +
+                        " bytes of workspace, above the fixed " + std::to_string(kScratchBytes) +
+                        "-byte scratch; use tg_gemm or tg_gemm_ws");
+    rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    if (empty) return TG_OK;
+    void* ws = nullptr;
+    rc = scratch_address(device, &ws);
+    if (rc != TG_OK) return rc;
+    return run_gemm(semiring, dtype, p, ws, kScratchBytes, as_stream(stream));
 }
 
 size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,
