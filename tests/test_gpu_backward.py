@@ -349,3 +349,43 @@ def test_dlpack_and_numpy_faces():
     assert tuple(c3.shape) == (2, 5, 4)
     with pytest.raises(RuntimeError, match="GPU device"):
         tgm.maxplus_matmul_batched_dlpack(a3.cpu(), b3.cpu())
+
+
+def _assert_bits_nan(got, ref):
+    """Same NaN positions, every other element bit-exact (NaN payloads may
+    differ between the CPU and the GPU)."""
+    got, ref = np.ascontiguousarray(got), np.ascontiguousarray(ref)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(tc.bits(got[~nan]), tc.bits(ref[~nan]))
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("k", [64, 4096, 70000])
+def test_backward_signed_zero_inf_nan(dtype, k):
+    """dC holding -0.0, +-inf and NaN, with bins repeated inside blocks: the
+    sums start from +0.0 (a bin fed only -0.0 ends +0.0), infinities of both
+    signs meet (NaN), and NaN spreads to the bins it reaches, as in the
+    reference's sequential sums.  Covers the LDS and the global-bin kernels."""
+    from tropical_gemm import ops
+
+    m, n = 70, 300
+    rng = np.random.default_rng(k + 3)
+    g = rng.standard_normal((m, n)).astype(dtype)
+    am = rng.integers(0, min(k, 24), size=(m, n)).astype(np.int32)
+    g[rng.random((m, n)) < 0.2] = -0.0
+    g[rng.random((m, n)) < 0.01] = np.inf
+    g[rng.random((m, n)) < 0.01] = -np.inf
+    g[rng.random((m, n)) < 0.005] = np.nan
+    am[5, :] = 3
+    g[5, :] = -0.0  # a bin fed only -0.0
+    print(f"[case] signed zero / inf / nan {np.dtype(dtype).name} k={k}", flush=True)
+    tg_, tam = torch.from_numpy(g).to(DEV), torch.from_numpy(am).to(DEV)
+    ga = ops.backward_a(tg_, tam, k).cpu().numpy()
+    gb = ops.backward_b(tg_, tam, k).cpu().numpy()
+    ga_ref = oracle.backward_a(g, am.astype(np.uint32), k)
+    gb_ref = oracle.backward_b(g, am.astype(np.uint32), k)
+    assert np.isnan(ga_ref).any() and np.isinf(ga_ref).any()
+    assert tc.bits(ga_ref[5:6, 3:4])[0, 0] == 0  # +0.0
+    _assert_bits_nan(ga, ga_ref)
+    _assert_bits_nan(gb, gb_ref)

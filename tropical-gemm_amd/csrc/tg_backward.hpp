@@ -12,46 +12,41 @@
 // is bit-identical to the reference and the same from run to run.
 //
 // Ordering inside a wave: a block of 64 consecutive contributions (one per
-// lane, in lane order) is grouped by target bin with 64-bit ballots over the
-// bits of the bin index (wave_match_rank: a lane's rank is the number of
-// earlier lanes with the same bin); then the block is applied in rounds,
-// round r adding the contributions of rank r.  Within a round all targets
-// differ, and the rounds run in program order, so each bin sees its
-// contributions in lane order; blocks run in sequence.  A block costs one
-// round per repetition of its most repeated bin (one or two for spread
-// indices); a block that repeats a bin more than kRoundsMax times sums each
-// bin serially in a wave-uniform register instead (a near-constant argmax:
-// the sequential chain the sum needs anyway).
+// lane, in lane order) is grouped by target bin, and the lowest lane of each
+// group (its leader) applies the group: bin + g(leader) + g(2nd) + ... in
+// lane order, one read and one write of the bin.  Groups have distinct bins,
+// so they run side by side; blocks run in sequence.
+//   * Grouping with LDS bins (lds_group): every active lane saves its bin's
+//     value, zeroes the bin, ORs its lane bit into it and reads it back,
+//     which leaves each lane the mask of the lanes sharing its bin (f32 bins
+//     hold 32 bits: two halves of the wave in turn; f64 bins one 64-bit OR).
+//     Seven (four) LDS instructions, one round trip.  With bins in global
+//     memory (K too large for LDS) the mask comes from 64-bit ballots over
+//     the bits of the bin index instead (wave_match_mask).
+//   * Summing (group_sum): in passes of kStageRanks ranks, each member of
+//     rank r0 + u posts its value to row u, column leader, of a per-wave LDS
+//     stage, and every leader reads its column: kStageRanks values, the
+//     missing ranks +0.0.  Adding +0.0 never changes a running sum that
+//     starts from +0.0 (such a sum is never -0.0 under round-to-nearest), so
+//     the leader adds every row unconditionally.  Readers clear their column
+//     behind them, so the stage is all +0.0 between passes.
 //
-// grad_A (tg_bwd_rows): one wave per row of C at a time, its K bins in LDS
-// (rows are independent; the wave walks j in blocks of 64).
-// grad_B (tg_bwd_cols): one wave per column of C, its K bins in LDS; a
-// workgroup of W waves takes W adjacent columns and stages 64-row tiles of
-// argmax and dC for them through LDS (coalesced row segments), and each wave
-// walks i in blocks of 64.
-// Both loop over their rows/columns with a grid stride, so any M, N and batch
-// fit the launch (grid sizes come from bwd_*_geometry on the host).  Bins
-// that do not fit LDS live in the gradient itself (GLOBAL instantiations):
-// the same order, with coherent loads and stores to global memory.
 #pragma once
 
 #include "tg_kernels.hpp"
 
 namespace tg {
 
-// Rank of this lane's key among the active lanes of the wave holding the
-// same key (the number of lower lanes with an equal key).  nbits: bits that
-// can differ between keys (keys < 2^nbits).
-__device__ __forceinline__ int wave_match_rank(uint32_t key, bool active, int nbits) {
+// Mask of the active lanes whose key equals this lane's (0 for an inactive
+// lane).  nbits: bits that can differ between keys (keys < 2^nbits).
+__device__ __forceinline__ uint64_t wave_match_mask(uint32_t key, bool active, int nbits) {
     uint64_t match = __ballot(active);
     for (int b = 0; b < nbits; ++b) {
         const bool bit = (key >> b) & 1u;
         const uint64_t m = __ballot(active && bit);
         match &= bit ? m : ~m;
     }
-    const int lane = threadIdx.x & 63;
-    const uint64_t below = lane == 0 ? 0 : (~uint64_t(0) >> (64 - lane));
-    return __popcll(match & below);
+    return active ? match : 0;
 }
 
 // Bits needed for keys in [0, K).
@@ -61,87 +56,136 @@ __host__ __device__ inline int key_bits(int64_t K) {
     return b;
 }
 
-// Wave-wide maximum of a small non-negative int.
-__device__ __forceinline__ int wave_max(int x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const int y = __shfl_xor(x, off, 64);
-        x = y > x ? y : x;
-    }
-    return x;
+// Relaxed LDS accesses for the grouping steps: atomics, so the compiler
+// keeps every step (no store-to-load forwarding across another lane's OR).
+template <typename U>
+__device__ __forceinline__ U lds_ld(U* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+template <typename U>
+__device__ __forceinline__ void lds_st(U* p, U v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+template <typename U>
+__device__ __forceinline__ void lds_or(U* p, U v) {
+    __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
-// Lane l's value of x (wave-uniform result).
+// Groups the active lanes by LDS bin (see the header comment): returns the
+// mask of the active lanes whose key equals this lane's (0 when inactive)
+// and the bin's value before this block in `before`.  Leaves garbage in the
+// touched bins: the leaders overwrite them (lds_apply).
 template <typename T>
-__device__ __forceinline__ T read_lane(T x, int l) {
-    if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+__device__ __forceinline__ uint64_t lds_group(T* bins, int32_t key, bool active, T& before) {
+    const int lane = threadIdx.x & 63;
+    uint64_t m = 0;
+    before = T(0);
+    if constexpr (sizeof(T) == 8) {
+        uint64_t* slot = reinterpret_cast<uint64_t*>(bins) + (active ? key : 0);
+        if (active) {
+            before = __builtin_bit_cast(T, lds_ld(slot));
+            lds_st(slot, uint64_t(0));
+            lds_or(slot, uint64_t(1) << lane);
+            m = lds_ld(slot);
+        }
     } else {
-        const uint64_t u = __builtin_bit_cast(uint64_t, x);
-        const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(u), l);
-        const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(u >> 32), l);
-        return __builtin_bit_cast(T, (uint64_t(hi) << 32) | lo);
+        uint32_t* slot = reinterpret_cast<uint32_t*>(bins) + (active ? key : 0);
+        uint32_t lo = 0, hi = 0;
+        if (active) {
+            before = __builtin_bit_cast(T, lds_ld(slot));
+            lds_st(slot, 0u);
+        }
+        if (active && lane < 32) lds_or(slot, 1u << lane);
+        if (active) {
+            lo = lds_ld(slot);
+            lds_st(slot, 0u);
+        }
+        if (active && lane >= 32) lds_or(slot, 1u << (lane - 32));
+        if (active) hi = lds_ld(slot);
+        m = (uint64_t(hi) << 32) | lo;
     }
+    return m;
 }
 
-// bins[key * es] += g in lane order among equal keys (see the header
-// comment).  Up to kRoundsMax repetitions of a key: rounds of distinct-bin
-// read-add-writes.  A block that repeats one bin more often than that (a
-// near-constant argmax) sums each bin's contributions serially instead: the
-// bin is read once, its lanes' values are added one by one in lane order in
-// a wave-uniform register, and the sum is written once.
-// GLOBAL: the bins are in global memory, read and written with relaxed
-// device-scope atomics (coherent, in this wave's program order per address).
-constexpr int kRoundsMax = 8;
+// Ranks per stage pass, and the stage's size per wave in elements.
+constexpr int kStageRanks = 4;
+constexpr int kStageElems = kStageRanks * 64;
 
-template <typename T, bool GLOBAL>
-__device__ __forceinline__ void ordered_add(T* bins, int64_t es, int32_t key, T g, bool active,
-                                            int rank) {
-    auto ld = [&](int64_t k) {
-        if constexpr (GLOBAL)
-            return __hip_atomic_load(bins + k * es, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            return bins[k];
-    };
-    auto st = [&](int64_t k, T v) {
-        if constexpr (GLOBAL)
-            __hip_atomic_store(bins + k * es, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-            bins[k] = v;
-    };
-    // Global bins: this wave's stores complete before its next loads, so a
-    // bin written by one lane is read back by another from L2.
-    auto order = [&]() {
-        if constexpr (GLOBAL) __threadfence_block();
-    };
-    if (wave_max(active ? rank : 0) < kRoundsMax) {
-        for (int r = 0;; ++r) {
-            const bool go = active && rank == r;
-            if (__ballot(go) == 0) break;
-            if (go) st(key, ld(key) + g);
-            order();
+// The leader's sum before + g(leader) + g(rank 1) + g(rank 2) + ... of its
+// group (m: this lane's group mask, 0 when inactive); meaningful on leaders
+// only.  stage: this wave's kStageElems elements, all +0.0 on entry and on
+// return.  Wave-uniform: call with the whole wave active.
+template <typename T>
+__device__ __forceinline__ T group_sum(uint64_t m, T g, T before, bool& leader, T* stage) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t rank =
+        __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
+    leader = m != 0 && rank == 0;
+    const int size = __popcll(m);
+    T acc = before + g;
+    if (__ballot(leader && size > 1)) {
+        const int lead = m != 0 ? int(__builtin_ctzll(m)) : 0;
+        for (int r0 = 1; __ballot(leader && size > r0); r0 += kStageRanks) {
+            const uint32_t d = rank - uint32_t(r0);
+            if (m != 0 && d < uint32_t(kStageRanks)) lds_st(stage + d * 64 + lead, g);
+            T v[kStageRanks];
+#pragma unroll
+            for (int u = 0; u < kStageRanks; ++u) v[u] = lds_ld(stage + u * 64 + lane);
+#pragma unroll
+            for (int u = 0; u < kStageRanks; ++u) lds_st(stage + u * 64 + lane, T(0));
+#pragma unroll
+            for (int u = 0; u < kStageRanks; ++u) acc = acc + v[u];
         }
-        return;
     }
-    uint64_t todo = __ballot(active);
-    while (todo) {
-        const int leader = __builtin_ctzll(todo);
-        const int32_t k = __builtin_amdgcn_readlane(key, leader);
-        uint64_t grp = __ballot(active && key == k);
-        todo &= ~grp;
-        T acc = read_lane(ld(k), 0);  // every lane read the same bin
-        while (grp) {
-            acc = acc + read_lane(g, __builtin_ctzll(grp));
-            grp &= grp - 1;
-        }
-        if ((threadIdx.x & 63) == 0) st(k, acc);
-        order();
-    }
+    return acc;
+}
+
+// Zeroes this wave's stage.
+template <typename T>
+__device__ __forceinline__ void stage_clear(T* stage) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int u = 0; u < kStageRanks; ++u) lds_st(stage + u * 64 + lane, T(0));
+}
+
+// bins[key] += g in lane order among equal keys, bins in LDS.  Wave-uniform.
+template <typename T>
+__device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active) {
+    T before;
+    const uint64_t m = lds_group(bins, key, active, before);
+    bool leader;
+    const T acc = group_sum(m, g, before, leader, stage);
+    if (leader) lds_st(reinterpret_cast<T*>(bins) + key, acc);
+}
+
+// bins[key * es] += g in lane order among equal keys, bins in global memory
+// (read and written by the leaders with relaxed device-scope atomics).  The
+// next block's leader for a bin may be another lane, so the trailing
+// device-scope fence waits until this block's writes have reached L2 before
+// the wave issues its next reads (a workgroup-scope fence does not wait for
+// them).  Wave-uniform.
+template <typename T>
+__device__ __forceinline__ void global_apply(T* bins, T* stage, int64_t es, int32_t key, T g,
+                                             bool active, int nbits) {
+    const uint64_t m = wave_match_mask(uint32_t(key), active, nbits);
+    const int lane = threadIdx.x & 63;
+    const bool first = m != 0 && int(__builtin_ctzll(m)) == lane;
+    T before = T(0);
+    if (first)
+        before = __hip_atomic_load(bins + int64_t(key) * es, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    bool leader;
+    const T acc = group_sum(m, g, before, leader, stage);
+    if (leader)
+        __hip_atomic_store(bins + int64_t(key) * es, acc, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    __threadfence();
 }
 
 // ---------------------------------------------------------------------------
 // grad_A.  rows = batch * M; row rr is (z = rr / M, i = rr % M).  Each wave
-// owns one row at a time; LDS: K bins per wave (dynamic, waves * K * T).
+// owns one row at a time; LDS: K bins per wave (not with GLOBAL), then a
+// stage of kStageElems per wave: waves * (K + kStageElems) * sizeof(T).
 //   MULT: MaxMul rule, g *= B[z][k][j] (OTHER = B, row-major K x N).
 // GLOBAL: the bins are the grad_A row itself (K too large for LDS).
 // grid: any size (grid-stride over rows), block = 64 * waves.
@@ -157,6 +201,10 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
     const int wave = threadIdx.x >> 6;
     const int waves = blockDim.x >> 6;
     const int nbits = key_bits(K);
+    constexpr int PF = 8;  // blocks of 64 contributions per prefetch chunk
+    const int64_t bins_elems = GLOBAL ? 0 : int64_t(waves) * K;
+    T* stage = reinterpret_cast<T*>(bwd_lds) + bins_elems + int64_t(wave) * kStageElems;
+    stage_clear(stage);
     for (int64_t rr = int64_t(blockIdx.x) * waves + wave; rr < rows;
          rr += int64_t(gridDim.x) * waves) {
         const int64_t z = rr / M, i = rr - z * M;
@@ -168,23 +216,47 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
         if constexpr (GLOBAL) {
             for (int64_t k = lane; k < K; k += 64)
                 __hip_atomic_store(bins + k, T(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __threadfence();  // zeros visible to every lane's first read
         } else {
             for (int64_t k = lane; k < K; k += 64) bins[k] = T(0);
         }
-        // Contributions in blocks of 64 consecutive j, the next block's
-        // loads issued before the current one is applied.
-        int32_t kn = lane < N ? k_row[lane] : -1;
-        T gn = lane < N ? g_row[lane] : T(0);
-        for (int64_t j0 = 0; j0 < N; j0 += 64) {
-            const int32_t key = kn;
-            T g = gn;
-            const int64_t jn = j0 + 64 + lane;
-            kn = jn < N ? k_row[jn] : -1;
-            gn = jn < N ? g_row[jn] : T(0);
-            const bool active = key >= 0 && int64_t(key) < K;
-            if (MULT && active) g = g * other[int64_t(key) * N + j0 + lane];
-            const int rank = wave_match_rank(uint32_t(key), active, nbits);
-            ordered_add<T, GLOBAL>(bins, 1, key, g, active, rank);
+        // Contributions in chunks of PF blocks of 64 consecutive j.  The next
+        // chunk's loads are issued before the current chunk is applied
+        // (unconditional loads of clamped columns, so each wait covers only
+        // the older chunk), which hides the global latency behind PF blocks
+        // of work; the MaxMul factors of a chunk are gathered at its start.
+        auto load_chunk = [&](int64_t j0, int32_t (&kk)[PF], T (&gg)[PF]) {
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                const int64_t j = j0 + 64 * u + lane;
+                kk[u] = k_row[j < N ? j : N - 1];
+                gg[u] = g_row[j < N ? j : N - 1];
+            }
+        };
+        int32_t kc[PF], kn[PF];
+        T gc[PF], gn[PF];
+        load_chunk(0, kc, gc);
+        for (int64_t j0 = 0; j0 < N; j0 += 64 * PF) {
+            load_chunk(j0 + 64 * PF, kn, gn);
+            bool act[PF];
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                act[u] = j0 + 64 * u + lane < N && kc[u] >= 0 && int64_t(kc[u]) < K;
+                if (MULT && act[u]) gc[u] = gc[u] * other[int64_t(kc[u]) * N + j0 + 64 * u + lane];
+            }
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                if (j0 + 64 * u >= N) break;
+                if constexpr (GLOBAL)
+                    global_apply<T>(bins, stage, 1, kc[u], gc[u], act[u], nbits);
+                else
+                    lds_apply<T>(bins, stage, kc[u], gc[u], act[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                kc[u] = kn[u];
+                gc[u] = gn[u];
+            }
         }
         if constexpr (!GLOBAL) {
             for (int64_t k = lane; k < K; k += 64) out[k] = bins[k];
@@ -196,14 +268,24 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
 // grad_B.  Column groups: batch * ceil(N / W) groups of W adjacent columns,
 // W = waves per workgroup; group gg is (z = gg / groups_n, columns
 // c0 = (gg % groups_n) * W ...).  Wave w owns column c0 + w and its K bins
-// (LDS, or the grad_B column itself with GLOBAL).  Per 64-row block the
-// workgroup stages argmax and dC for its W columns in LDS (row stride W + 1:
-// the column reads of 64 lanes hit distinct banks), then each wave applies
-// its column's 64 contributions in row order.
+// (LDS, or the grad_B column itself with GLOBAL).  The workgroup stages
+// argmax and dC for its W columns in tiles of kBwdTileRows rows through LDS
+// (row stride W + 1: the column reads of 64 lanes hit distinct banks); each
+// wave then applies its column's tile in blocks of 64 rows, in row order.
+// Every thread stages kBwdTileRows / 64 elements per tile and loads the next
+// tile's into registers before the current tile is applied (unconditional
+// loads of a clamped row and column), so the global latency hides behind a
+// tile of bin updates and the waves meet at a barrier once per tile.
+// Workgroups on one XCD (launch order b, b + 8, b + 16, ...) take adjacent
+// column groups, so the W-column segments that share a cache line are read
+// and written through one L2.
 //   MULT: MaxMul rule, g *= A[z][i][k] (OTHER = A, row-major M x K).
-// LDS: W * K bins (not with GLOBAL) + 64 (W + 1) (4 + sizeof(T)) bytes.
+// LDS: W * K bins (not with GLOBAL), the tile, kBwdTileRows (W + 1) (4 +
+// sizeof(T)) bytes, then a stage of kStageElems per wave.
 // grid: any size (grid-stride over column groups), block = 64 * W, W <= 8.
 // ---------------------------------------------------------------------------
+constexpr int kBwdTileRows = 256;
+
 template <typename T, bool MULT, bool GLOBAL>
 __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                                                    const int32_t* __restrict__ IDX,
@@ -211,6 +293,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                                                    int64_t N, int64_t K, int64_t sC, int64_t sO,
                                                    int64_t sB, int64_t groups_n, int64_t groups) {
     extern __shared__ __align__(16) unsigned char bwd_lds[];
+    constexpr int TB = kBwdTileRows / 64;  // blocks of 64 rows per tile
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -220,8 +303,20 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
     T* bins_all = reinterpret_cast<T*>(bwd_lds);
     const int64_t bins_bytes = GLOBAL ? 0 : int64_t(W) * K * int64_t(sizeof(T));
     T* tile_g = reinterpret_cast<T*>(bwd_lds + bins_bytes);
-    int32_t* tile_k = reinterpret_cast<int32_t*>(bwd_lds + bins_bytes + 64 * stride * sizeof(T));
-    for (int64_t gg = blockIdx.x; gg < groups; gg += gridDim.x) {
+    int32_t* tile_k =
+        reinterpret_cast<int32_t*>(bwd_lds + bins_bytes + kBwdTileRows * stride * sizeof(T));
+    T* stage = reinterpret_cast<T*>(bwd_lds + bins_bytes +
+                                    kBwdTileRows * stride * (sizeof(T) + 4)) +
+               wave * kStageElems;
+    stage_clear(stage);
+    // This thread's staging slots: rows sr + 64 t (t < TB), column sq.
+    const int sr = tid / W, sq = tid - (tid / W) * W;
+    // XCD-aware order: with a grid that is a multiple of 8, launch slot b
+    // (on XCD b % 8) takes rank (b % 8) * (grid / 8) + b / 8.
+    const int64_t grid = gridDim.x;
+    const int64_t b = blockIdx.x;
+    const int64_t first = (grid % 8 == 0) ? (b % 8) * (grid / 8) + b / 8 : b;
+    for (int64_t gg = first; gg < groups; gg += grid) {
         const int64_t z = gg / groups_n;
         const int64_t c0 = (gg - z * groups_n) * W;
         const int64_t c = c0 + wave;
@@ -236,31 +331,55 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                 for (int64_t k = lane; k < K; k += 64)
                     __hip_atomic_store(bins + k * es, T(0), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
+                __threadfence();
             } else {
                 for (int64_t k = lane; k < K; k += 64) bins[k] = T(0);
             }
         }
-        for (int64_t i0 = 0; i0 < M; i0 += 64) {
-            // Stage the 64 x W block (row i0 + r, column c0 + q) of argmax and dC.
-            for (int e = tid; e < 64 * W; e += blockDim.x) {
-                const int r = e / W, q = e - (e / W) * W;
-                const int64_t i = i0 + r, cc = c0 + q;
+        const int64_t cc = c0 + sq;
+        const int64_t ccl = cc < N ? cc : N - 1;
+        int32_t kr[TB];
+        T gr[TB];
+        auto stage_load = [&](int64_t i0) {
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                const int64_t i = i0 + 64 * t + sr;
+                const int64_t il = i < M ? i : M - 1;
                 const bool ok = i < M && cc < N;
-                tile_k[r * stride + q] = ok ? kz[i * N + cc] : -1;
-                tile_g[r * stride + q] = ok ? gz[i * N + cc] : T(0);
+                const int32_t kl = kz[il * N + ccl];
+                const T gl = gz[il * N + ccl];
+                kr[t] = ok ? kl : -1;
+                gr[t] = ok ? gl : T(0);
+            }
+        };
+        stage_load(0);
+        for (int64_t i0 = 0; i0 < M; i0 += kBwdTileRows) {
+            __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+                tile_k[(64 * t + sr) * stride + sq] = kr[t];
+                tile_g[(64 * t + sr) * stride + sq] = gr[t];
             }
             __syncthreads();
+            stage_load(i0 + kBwdTileRows);
             if (c < N) {
-                const int32_t key = tile_k[lane * stride + wave];
-                T g = tile_g[lane * stride + wave];
-                const bool active = key >= 0 && int64_t(key) < K;
-                if (MULT && active) g = g * other[(i0 + lane) * K + key];
-                const int rank = wave_match_rank(uint32_t(key), active, nbits);
-                ordered_add<T, GLOBAL>(bins, es, key, g, active, rank);
+#pragma unroll
+                for (int t = 0; t < TB; ++t) {
+                    const int64_t it = i0 + 64 * t;
+                    if (it >= M) break;
+                    const int32_t key = tile_k[(64 * t + lane) * stride + wave];
+                    T g = tile_g[(64 * t + lane) * stride + wave];
+                    const bool active = key >= 0 && int64_t(key) < K;
+                    if (MULT && active) g = g * other[(it + lane) * K + key];
+                    if constexpr (GLOBAL)
+                        global_apply<T>(bins, stage, es, key, g, active, nbits);
+                    else
+                        lds_apply<T>(bins, stage, key, g, active);
+                }
             }
-            __syncthreads();
         }
         if constexpr (!GLOBAL) {
+            __syncthreads();  // every wave's bins are complete
             // The W columns leave together: row k of the group is W
             // consecutive elements of grad_B.
             for (int64_t e = tid; e < int64_t(W) * K; e += blockDim.x) {
@@ -268,8 +387,8 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                 const int q = int(e - k * W);
                 if (c0 + q < N) outz[k * N + c0 + q] = bins_all[int64_t(q) * K + k];
             }
-            __syncthreads();  // the next group zeroes the bins
         }
+        __syncthreads();  // the next group zeroes the bins and restages
     }
 }
 

@@ -928,7 +928,8 @@ size_t scratch_need(tg_dtype dt, const Problem& p, const Plan& pl) {
 // the grid is capped (kBwdMaxGrid workgroups) and no dimension of a launch
 // grows with M, N or the batch.
 constexpr int64_t kBwdMaxGrid = 16384;
-constexpr size_t kBwdLdsBudget = 128 * 1024;  // per workgroup, of the CU's 160 KB
+constexpr size_t kBwdLdsBudget = 128 * 1024;  // bins of one grad_A row at most
+constexpr size_t kBwdLdsLimit = 160 * 1024;   // the CU's LDS
 
 struct BwdGeometry {
     bool global = false;  // bins in the gradient itself (K too large for LDS)
@@ -939,40 +940,47 @@ struct BwdGeometry {
     int64_t groups = 0;   // grad_B: column groups in total
 };
 
-// grad_A: one wave per row; two waves per workgroup (32 KB of bins each at
-// K = 4096 f32, five workgroups per CU), one wave when a row's bins need
-// more than 64 KB, global bins beyond the LDS budget.
+// grad_A: one wave per row; a wave's LDS is its row's K bins plus its stage
+// (tg::kStageElems elements).  Four waves per workgroup while that is at
+// most 8 KB, two while at most 16 KB, else one (17 KB at K = 4096 f32: nine
+// workgroups per CU); global bins beyond the LDS budget.
 BwdGeometry bwd_rows_geometry(int64_t rows, int64_t K, size_t es) {
     BwdGeometry g;
     const size_t row_bytes = size_t(K) * es;
-    if (row_bytes <= 32 * 1024) {
-        g.waves = 2;
-    } else if (row_bytes <= kBwdLdsBudget) {
-        g.waves = 1;
-    } else {
+    const size_t stage_bytes = size_t(tg::kStageElems) * es;
+    const size_t wave_bytes = row_bytes + stage_bytes;
+    if (row_bytes > kBwdLdsBudget) {
         g.global = true;
         g.waves = 4;
+    } else {
+        g.waves = wave_bytes <= 8 * 1024 ? 4 : wave_bytes <= 16 * 1024 ? 2 : 1;
     }
-    g.lds = g.global ? 0 : size_t(g.waves) * row_bytes;
+    g.lds = size_t(g.waves) * (g.global ? stage_bytes : wave_bytes);
     const int64_t need = (rows + g.waves - 1) / g.waves;
     g.grid = need < kBwdMaxGrid ? need : kBwdMaxGrid;
     return g;
 }
 
-// grad_B: one wave per column, W <= 8 adjacent columns per workgroup, as
-// many as their bins fit the LDS budget (8 at K = 4096 f32), plus the staged
-// 64 x W tiles of argmax and dC.
+// grad_B: one wave per column, W <= 8 adjacent columns per workgroup: the
+// most whose bins, the staged tiles of argmax and dC (tg::kBwdTileRows x W)
+// and the waves' stages fit the CU's 160 KB (8 at K = 4096 f32: 154 KB);
+// global bins when not even one column's fit.
 BwdGeometry bwd_cols_geometry(int64_t batch, int64_t N, int64_t K, size_t es) {
     BwdGeometry g;
     const size_t col_bytes = size_t(K) * es;
-    int64_t w = col_bytes > 0 ? int64_t(kBwdLdsBudget / col_bytes) : 8;
-    if (w > 8) w = 8;
+    auto lds_for = [&](int64_t w, bool global) {
+        return (global ? 0 : size_t(w) * col_bytes) +
+               size_t(tg::kBwdTileRows) * size_t(w + 1) * (4 + es) +
+               size_t(w) * size_t(tg::kStageElems) * es;
+    };
+    int64_t w = col_bytes > kBwdLdsBudget ? 0 : 8;
+    while (w >= 1 && lds_for(w, false) > kBwdLdsLimit) --w;
     if (w < 1) {
         g.global = true;
         w = 8;
     }
     g.waves = int(w);
-    g.lds = (g.global ? 0 : size_t(w) * col_bytes) + 64 * size_t(w + 1) * (4 + es);
+    g.lds = lds_for(w, g.global);
     g.groups_n = (N + w - 1) / w;
     g.groups = batch * g.groups_n;
     g.grid = g.groups < kBwdMaxGrid ? g.groups : kBwdMaxGrid;
@@ -995,7 +1003,8 @@ int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t b
     if (g.grid == 0) return TG_OK;
     if (g.global) {
         hipLaunchKernelGGL((tg::tg_bwd_rows<T, MULT, true>), dim3(unsigned(g.grid)),
-                           dim3(64 * g.waves), 0, st, G, I, O, GA, M, N, K, sC, sO, sA, batch * M);
+                           dim3(64 * g.waves), g.lds, st, G, I, O, GA, M, N, K, sC, sO, sA,
+                           batch * M);
     } else {
         int rc = allow_lds(&tg::tg_bwd_rows<T, MULT, false>, g.lds);
         if (rc != TG_OK) return rc;
