@@ -564,44 +564,73 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                     list[atomicAdd(&hist[ch[i][j] >> shift], 1u)] = uint16_t(trow(i) * BN + tcol(j));
         __syncthreads();
 
-        // Resolve, chunk-sorted, one output per thread at a time.
+        // Resolve, chunk-sorted, one output per thread at a time, the next
+        // output's windows loading while the current one is scanned (loads
+        // of a list entry this thread owns, unconditional, so each wait
+        // covers only the older pair).
         constexpr int NW = CL / 4;
-        for (int e = tid; e < total; e += TG_THREADS) {
+        struct Window {
+            Vec16<T> a[NW], b[NW];
+        };
+        auto window_ptrs = [&](int e, const T*& ap, const T*& bp) {
             const int lid = int(list[e]);
             const int64_t c = int64_t(chs[lid]);
             // Clamped like the tile loads (outputs past M or N are not
-            // stored; their windows just stay in bounds).  Quads of a window
-            // past K read the row's last quad: duplicates that come after
-            // their originals, so the first match is a k < K.
+            // stored; their windows just stay in bounds).
             const int64_t gr = row0 + lid / BN, gc = col0 + (lid & (BN - 1));
-            const T* ap = A + (gr < M ? gr : M - 1) * K + c * CL;
-            const T* bp = BT + (gc < N ? gc : N - 1) * K + c * CL;
-            T p[CL];
+            ap = A + (gr < M ? gr : M - 1) * K + c * CL;
+            bp = BT + (gc < N ? gc : N - 1) * K + c * CL;
+            return c;
+        };
+        auto load_window = [&](int e, Window& wv) {
+            const T* ap;
+            const T* bp;
+            const int64_t c = window_ptrs(e, ap, bp);
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
+                // Quads of a window past K read the row's last quad:
+                // duplicates that come after their originals, so the first
+                // match is a k < K.
                 const int64_t off = (!TAILK || c * CL + w * 4 <= K - 4) ? w * 4 : K - 4 - c * CL;
-                const Vec16<T> av = *reinterpret_cast<const Vec16<T>*>(ap + off);
-                const Vec16<T> bv = *reinterpret_cast<const Vec16<T>*>(bp + off);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) p[w * 4 + q] = tmul<SR, T>(av.v[q], bv.v[q]);
+                wv.a[w] = *reinterpret_cast<const Vec16<T>*>(ap + off);
+                wv.b[w] = *reinterpret_cast<const Vec16<T>*>(bp + off);
             }
-            T mx = tjoin<SR, T>(p[0], p[1]);
+        };
+        if (tid < total) {
+            Window cur;
+            load_window(tid, cur);
+            for (int e = tid; e < total; e += TG_THREADS) {
+                // The next entry this thread owns, or this one again (its
+                // chunk slot is overwritten only below): never another
+                // thread's entry, whose slot may already hold an offset.
+                const int en = e + TG_THREADS < total ? e + TG_THREADS : e;
+                Window nxt;
+                load_window(en, nxt);
+                T p[CL];
 #pragma unroll
-            for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
-            // Last match scanning downwards == first match; groups of 8
-            // compares keep few lane masks live at once.
-            int f = 0;
+                for (int w = 0; w < NW; ++w)
 #pragma unroll
-            for (int q = CL / 8 - 1; q >= 0; --q) {
+                    for (int q = 0; q < 4; ++q) p[w * 4 + q] = tmul<SR, T>(cur.a[w].v[q], cur.b[w].v[q]);
+                T mx = tjoin<SR, T>(p[0], p[1]);
 #pragma unroll
-                for (int kk = q * 8 + 7; kk >= q * 8; --kk) f = (p[kk] == mx) ? kk : f;
-                __builtin_amdgcn_sched_barrier(0);
+                for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
+                // First match: independent match bits, then the lowest.
+                uint32_t bits = 0;
+#pragma unroll
+                for (int kk = 0; kk < CL; ++kk) bits |= (p[kk] == mx) ? (1u << kk) : 0u;
+                const int f = bits ? int(__builtin_ctz(bits)) : 0;
+                int r = f;
+                if constexpr (std::is_floating_point<T>::value) {
+                    if (mx == T(0)) {
+                        const T* ap;
+                        const T* bp;
+                        window_ptrs(e, ap, bp);
+                        if (__builtin_signbit(tmul<SR, T>(ap[f], bp[f]))) r |= 32;
+                    }
+                }
+                chs[int(list[e])] = uint16_t(r);
+                cur = nxt;
             }
-            int r = f;
-            if constexpr (std::is_floating_point<T>::value) {
-                if (mx == T(0) && __builtin_signbit(tmul<SR, T>(ap[f], bp[f]))) r |= 32;
-            }
-            chs[lid] = uint16_t(r);
         }
         __syncthreads();
 
