@@ -42,6 +42,11 @@ PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector (and dense) peak
 # lane-instructions/s) that is 157.3 * 2/3 = 104.9e12 tropical ops/s.
 TROP_PEAK_TOPS = PEAK_FP32_TFLOPS * 2 / 3
 PEAK_HBM_GBS = 8000.0         # MI355X published HBM3E bandwidth
+PEAK_FP64_TFLOPS = 78.6       # MI355X published FP64 vector peak
+# f64 has no three-input max: one v_add_f64 and one v_max_f64 per product
+# (2 tropical ops per 2 instructions) at the FP64 instruction peak (78.6
+# TFLOP/s = 39.3e12 FMA lane-instructions/s): 39.3e12 tropical ops/s.
+TROP_PEAK_F64_TOPS = PEAK_FP64_TFLOPS / 2
 DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
 WORKLOAD_NAMES = {
     "P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
@@ -51,6 +56,7 @@ WORKLOAD_NAMES = {
     "C4": "C4: MaxPlus i32 262144x128x128 +argmax",
     "C5": "C5: MaxPlus f32 4096^3 +argmax forward, then grad_A and grad_B backward",
     "M1": "M1: MaxPlus f32 65536x2048x8 +argmax (short K, HBM-bound)",
+    "F1": "F1: MaxPlus f64 4096^3 +argmax",
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
@@ -60,6 +66,7 @@ KERNEL_NAMES = {
     "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
+    "F1": "tg_gemm_tiles<MaxPlus, f64, argmax, chunked>",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
@@ -85,7 +92,7 @@ def cpu_model() -> str:
 # Rows of each configuration's CPU-baseline sample outside P (P: --cpu-rows):
 # about 0.5-4 s of single-core work.  C1 and C4 run whole; M1's short K makes
 # the reference's blocked loops slow (0.07 GOP/s), hence its small slab.
-CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096}
+CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096, "F1": 256}
 
 
 def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> dict:
@@ -243,7 +250,7 @@ def main() -> int:
     # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--config", default="P",
-                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "E1"])
+                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of P's CPU-baseline slab (0 skips the CPU baseline of every "
                          "configuration)")
@@ -367,17 +374,19 @@ def main() -> int:
                     "unit": "GB/s", "frac": round(kernel_gbs / PEAK_HBM_GBS, 4)}
     else:
         # Tropical (+)/(x) has no MFMA form: the kernel is bound by the
-        # vector ALU.  peak = MI355X published FP32 vector/dense peak.
-        roofline = {"bound": "valu", "achieved": round(kernel_tops, 3), "peak": PEAK_FP32_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(kernel_tops / PEAK_FP32_TFLOPS, 4)}
+        # vector ALU.  peak = MI355X published vector peak of the dtype.
+        peak = PEAK_FP64_TFLOPS if cfg["dtype"] == "f64" else PEAK_FP32_TFLOPS
+        roofline = {"bound": "valu", "achieved": round(kernel_tops, 3), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(kernel_tops / peak, 4)}
+    trop_peak = TROP_PEAK_F64_TOPS if cfg["dtype"] == "f64" else TROP_PEAK_TOPS
     roofline.update({
         "traffic": TRAFFIC.get(args.config),
         "kernel": KERNEL_NAMES[args.config],
         "kernel_ms": round(ms_kernel, 4),
         "kernel_launches_timed": int(nl.value),
         "ops_per_launch": ops,
-        "trop_peak": TROP_PEAK_TOPS,
-        "frac_of_trop_peak": round(kernel_tops / TROP_PEAK_TOPS, 4),
+        "trop_peak": trop_peak,
+        "frac_of_trop_peak": round(kernel_tops / trop_peak, 4),
         "algorithmic_bytes": algo_bytes,
     })
     out = {
@@ -397,7 +406,7 @@ def main() -> int:
                    "semiring": cfg["semiring"], "m": m, "n": n, "k": k,
                    "argmax": cfg["argmax"], "layout": "row-major", "parallelism": "none (1 GPU)"},
         "roofline": roofline,
-        "step_frac_of_trop_peak": round(gops / 1e3 / TROP_PEAK_TOPS, 4),
+        "step_frac_of_trop_peak": round(gops / 1e3 / trop_peak, 4),
         "wall_s_timed_region": round(wall, 4),
         "argmax_consistency_check": check,
         "device": torch.cuda.get_device_name(dev),

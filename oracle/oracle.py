@@ -57,7 +57,7 @@ def _load():
             fn = getattr(lib, name)
             fn.argtypes = [vp, vp, vp, vp, i64, i64, i64]
             fn.restype = None
-        for name in ("tgo_portable_argmax_f32", "tgo_portable_argmax_i32"):
+        for name in ("tgo_portable_argmax_f32", "tgo_portable_argmax_f64", "tgo_portable_argmax_i32"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.c_int, vp, vp, vp, vp, i64, i64, i64]
             fn.restype = ctypes.c_int
@@ -138,18 +138,20 @@ def backward_b(grad_c: np.ndarray, argmax: np.ndarray, k: int, a: np.ndarray | N
 
 def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
     """Single-thread restatement of the reference CPU argmax path (BLIS
-    PORTABLE tiling + 4x4 scalar microkernel) for float32 or int32 operands;
-    used as the timed baseline."""
+    PORTABLE tiling + 4x4 scalar microkernel) for float32, float64 or int32
+    operands; used as the timed baseline."""
     dt = np.dtype(a.dtype)
-    if dt not in (np.dtype(np.float32), np.dtype(np.int32)):
-        raise ValueError(f"portable baseline restated for float32 and int32, got {dt}")
+    if dt not in (np.dtype(np.float32), np.dtype(np.float64), np.dtype(np.int32)):
+        raise ValueError(f"portable baseline restated for float32, float64 and int32, got {dt}")
     a = np.ascontiguousarray(a, dtype=dt)
     b = np.ascontiguousarray(b, dtype=dt)
     m, k = a.shape
     n = b.shape[1]
     c = np.empty((m, n), dtype=dt)
     am = np.empty((m, n), dtype=np.uint32)
-    fn = _load().tgo_portable_argmax_f32 if dt == np.float32 else _load().tgo_portable_argmax_i32
+    fn = {np.dtype(np.float32): _load().tgo_portable_argmax_f32,
+          np.dtype(np.float64): _load().tgo_portable_argmax_f64,
+          np.dtype(np.int32): _load().tgo_portable_argmax_i32}[dt]
     rc = fn(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), _ptr(am), m, n, k)
     if rc != 0:
         raise ValueError("oracle rejected arguments")

@@ -30,7 +30,7 @@
  *     pthreads.  Results are therefore identical to the reference CPU path
  *     for every non-NaN input (NaN handling also follows the select rule).
  *
- *  2. tgo_portable_argmax_{f32,i32} and tgo_avx2_gemm_f32 : the CPU
+ *  2. tgo_portable_argmax_{f32,f64,i32} and tgo_avx2_gemm_f32 : the CPU
  *     BASELINES used for timing.  Faithful single-thread restatements of the
  *     reference's two CPU paths:
  *       argmax (every dtype): BLIS 5-loop with TilingParams::PORTABLE
@@ -356,6 +356,7 @@ TGO_BACKWARD_B(tgo_backward_b_f64, double)
     }
 
 TGO_PORTABLE(float, f32, zero_f32, mul_f32)
+TGO_PORTABLE(double, f64, zero_f64, mul_f64)
 TGO_PORTABLE(int32_t, i32, zero_i32, mul_i32)
 
 /* ------------------------------------------------------------------------ */

@@ -182,6 +182,20 @@ def test_portable_baseline_equals_oracle(sr):
 
 
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_portable_baseline_f64_equals_oracle(sr):
+    # Ties from a coarse grid; K = 300 crosses the 256-k block.
+    rng = np.random.default_rng(13)
+    a = np.round(rng.standard_normal((67, 300)) * 4) / 4
+    b = np.round(rng.standard_normal((300, 130)) * 4) / 4
+    if sr == "maxmul":
+        a, b = np.abs(a), np.abs(b)
+    c1, a1 = oracle.gemm(sr, a, b)
+    c2, a2 = oracle.portable_argmax(sr, a, b)
+    np.testing.assert_array_equal(tc.bits(c1), tc.bits(c2))
+    np.testing.assert_array_equal(a1, a2)
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
 def test_portable_baseline_i32_equals_oracle(sr):
     # K = 300 crosses the 256-k block (the argmax carries k_offset); ties,
     # and wrapping sums near the int32 limits.

@@ -12,6 +12,7 @@ the host) to the CPU oracle.  Nothing here reads the reference.
     C5  P forward, then backward with dC ~ N(0,1)
     M1  MaxPlus f32 M=65536 K=8 N=2048 with argmax, N(0,1): short K, bound by
         HBM (the 0.5 GB output and argmax writes), not by the VALU
+    F1  MaxPlus f64 4096^3 with argmax, A, B ~ N(0,1) (the f64 kernels)
     E1  tropical einsum "jik,lkj,lm->im", MaxPlus f32, N(0,1): i = l = m = 2048,
         j = 32, k = 64 (two 2048^3 contractions after two permutations)
 """
@@ -30,6 +31,7 @@ CONFIGS = {
     "C5": dict(semiring="maxplus", dtype="f32", m=4096, k=4096, n=4096, argmax=True,
                backward=True),
     "M1": dict(semiring="maxplus", dtype="f32", m=65536, k=8, n=2048, argmax=True, bound="hbm"),
+    "F1": dict(semiring="maxplus", dtype="f64", m=4096, k=4096, n=4096, argmax=True),
 }
 
 
@@ -47,9 +49,10 @@ def make_inputs(name: str, device="cuda", scale: float = 1.0):
     m = max(1, int(cfg["m"] * scale))
     k = cfg["k"] if name == "C4" else max(1, int(cfg["k"] * scale))
     n = cfg["n"] if name == "C4" else max(1, int(cfg["n"] * scale))
-    if name in ("P", "C1", "C5", "M1"):
-        a = torch.randn(m, k, generator=_gen(device, idx, 0), device=device)
-        b = torch.randn(k, n, generator=_gen(device, idx, 1), device=device)
+    if name in ("P", "C1", "C5", "M1", "F1"):
+        dt = torch.float64 if cfg["dtype"] == "f64" else torch.float32
+        a = torch.randn(m, k, generator=_gen(device, idx, 0), device=device, dtype=dt)
+        b = torch.randn(k, n, generator=_gen(device, idx, 1), device=device, dtype=dt)
     elif name == "C2":
         a = _distance_matrix(m, k, device, _gen(device, idx, 0), _gen(device, idx, 3))
         b = _distance_matrix(k, n, device, _gen(device, idx, 1), _gen(device, idx, 4))
