@@ -66,7 +66,7 @@ KERNEL_NAMES = {
     "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
-    "F1": "tg_gemm_tiles<MaxPlus, f64, argmax, chunked>",
+    "F1": "tg_gemm_dl64<MaxPlus> (f64, 64x128 tiles, argmax)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size

@@ -129,7 +129,8 @@ def test_python_layer_rejects_host_tensors():
     ("maxplus", "f32", 1024, 1024, 1024, True, "dl_4x4_cl8 split 4"),  # C1
     ("maxplus", "f32", 65536, 8, 2048, True, "shortk"),              # M1 (m, k, n order below)
     ("maxplus", "f32", 67, 45, 40, True, "tiles_exact"),
-    ("maxplus", "f64", 4096, 4096, 4096, True, "tiles_chunked"),
+    ("maxplus", "f64", 4096, 4096, 4096, True, "dl64_4x8_cl16"),
+    ("maxplus", "f64", 64, 64, 640, True, "tiles_chunked"),
 ])
 def test_gemm_plan_names_the_configured_paths(sr, dt, m, n, k, argmax, expected):
     if expected == "shortk":

@@ -1,0 +1,92 @@
+"""f64 direct-to-LDS argmax kernel (tg_gemm_dl64).
+
+Large f64 argmax problems run on it when the workspace holds B^T and the
+operand classes (tg_gemm_workspace_size); a workspace of only the B^T
+minimum runs the same product on the generic chunked kernel.  Both must give
+the same bits and argmax, equal to the oracle on sampled rows; NaN products
+(NaN operands, +inf meeting -inf, 0 * inf) follow the reference's serial
+rule through the class prepass and the serial rerun.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests import tg_cases as tc
+from tests.test_gpu_nan import nan_inputs
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _run(sr, a, b, full_ws):
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    m, k = a.shape
+    n = b.shape[1]
+    ws_bytes = (lib.tg_gemm_workspace_size(nat.DTYPE["f64"], 1, m, n, k, 1) if full_ws
+                else -(-(k * max(m, n) * 8) // 256) * 256)
+    plan = nat.gemm_plan(sr, "f64", m, n, k, True, workspace_bytes=ws_bytes)
+    ta = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    tb = torch.from_numpy(np.ascontiguousarray(b)).to(DEV)
+    c = torch.empty(m * n, dtype=torch.float64, device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=DEV)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    print(f"[case] dl64 {sr} {m}x{n}x{k} {plan}", flush=True)
+    nat.check(lib.tg_gemm_ws(0, nat.SEMIRING[sr], nat.DTYPE["f64"], 0, p(ta), p(tb), p(c), p(am),
+                             m, n, k, p(ws), ws_bytes, stream))
+    torch.cuda.synchronize()
+    return plan, c.cpu().numpy().reshape(m, n), am.cpu().numpy().reshape(m, n)
+
+
+def _check(c, am, c_ref, am_ref):
+    nan = np.isnan(c_ref)
+    np.testing.assert_array_equal(np.isnan(c), nan)
+    np.testing.assert_array_equal(tc.bits(c[~nan]), tc.bits(c_ref[~nan]))
+    np.testing.assert_array_equal(am.astype(np.int64), am_ref.astype(np.int64))
+
+
+def _operands(sr, m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    if sr == "maxmul":
+        a = 1.0 - rng.random((m, k))
+        b = 1.0 - rng.random((k, n))
+        a = np.round(a * 8) / 8 + 1 / 16  # ties, no zeros
+        b = np.round(b * 8) / 8 + 1 / 16
+    else:
+        a = np.round(rng.standard_normal((m, k)) * 4) / 4  # ties across k and chunks
+        b = np.round(rng.standard_normal((k, n)) * 4) / 4
+    return a, b
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+@pytest.mark.parametrize("m,n,k", [(1024, 4096, 640), (1000, 4092, 672)])
+def test_dl64_matches_generic_and_oracle(sr, m, n, k):
+    a, b = _operands(sr, m, n, k, seed=m + k)
+    plan, c, am = _run(sr, a, b, full_ws=True)
+    assert plan == "dl64_4x8_cl16"
+    plan0, c0, am0 = _run(sr, a, b, full_ws=False)
+    assert plan0 == "tiles_chunked"
+    _check(c, am, c0, am0)
+    rows = np.array([0, 1, 63, 64, 500, m - 1])
+    c_ref, am_ref = oracle.gemm(sr, a[rows], b)
+    _check(c[rows], am[rows], c_ref, am_ref)
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+def test_dl64_nan_rule(sr):
+    m, n, k = 1024, 4096, 640
+    a, b = nan_inputs(sr, np.float64, m, n, k, seed=17)
+    plan, c, am = _run(sr, a, b, full_ws=True)
+    assert plan == "dl64_4x8_cl16"
+    special = ~np.isfinite(a).all(axis=1) | (a == 0).any(axis=1)
+    rows = np.unique(np.concatenate([np.nonzero(special)[0], np.arange(0, m, 97), [m - 1]]))
+    c_ref, am_ref = oracle.gemm(sr, a[rows], b)
+    assert np.isnan(c_ref).any()
+    _check(c[rows], am[rows], c_ref, am_ref)

@@ -17,6 +17,7 @@
 #include "../../include/tropical_gemm_hip.h"
 #include "tg_backward.hpp"
 #include "tg_gemm_dl.hpp"
+#include "tg_gemm_dl64.hpp"
 #include "tg_gemm_kres.hpp"
 #include "tg_gemm_kres8.hpp"
 #include "tg_gemm_shortk.hpp"
@@ -196,6 +197,65 @@ WsLayout ws_layout(tg_dtype dt, int64_t batch, int64_t M, int64_t N, int64_t K, 
     w.pi = bt + part;
     w.total = bt + part + (argmax ? part : 0);
     return w;
+}
+
+// Workspace of the f64 direct-to-LDS argmax kernel: B^T (batch x K x N),
+// then the row classes of A (batch x M) and column classes of B (batch x N).
+size_t dl64_ws_bytes(int64_t batch, int64_t M, int64_t N, int64_t K) {
+    return round_up(size_t(batch) * size_t(K) * size_t(N) * 8, 256) +
+           round_up(size_t(batch) * size_t(M + N) * 4, 256);
+}
+
+// f64 argmax, large problems (tg_gemm_dl64): B^T staging and the operand
+// class prepass, then the GEMM.  K % 32 == 0 and the rest of dl64_fits hold.
+template <int SR>
+int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
+    using Cfg = tg::Dl64Cfg;
+    const int64_t tiles_m = (p.M + Cfg::BM - 1) / Cfg::BM;
+    const int64_t tiles_n = (p.N + Cfg::BN - 1) / Cfg::BN;
+    if (tiles_m * tiles_n > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "output too large for one launch");
+    if ((p.K + 31) / 32 > 65535 || (p.K + 255) / 256 > 65535)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the staging grids");
+    const double* A = static_cast<const double*>(p.A);
+    const double* B = static_cast<const double*>(p.B);
+    unsigned char* wsb = static_cast<unsigned char*>(ws);
+    double* BT = reinterpret_cast<double*>(wsb);
+    uint32_t* cls = reinterpret_cast<uint32_t*>(wsb + round_up(size_t(p.batch) * size_t(p.K) * size_t(p.N) * 8, 256));
+    uint32_t* clsA = cls;
+    uint32_t* clsB = cls + p.batch * p.M;
+    hipLaunchKernelGGL(tg::tg_fill_zero, dim3(unsigned((p.batch * (p.M + p.N) * 4 / 16 + 255) / 256 + 1)),
+                       dim3(256), 0, st, reinterpret_cast<unsigned char*>(cls), p.batch * (p.M + p.N) * 4);
+    TG_HIP(hipGetLastError());
+    {
+        int64_t blocks = (p.batch * p.M + 3) / 4;
+        if (blocks > 16384) blocks = 16384;
+        hipLaunchKernelGGL(tg::tg_class_rows, dim3(unsigned(blocks)), dim3(256), 0, st, A, p.M, p.K,
+                           p.sA, p.batch, clsA);
+        TG_HIP(hipGetLastError());
+    }
+    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+        dim3 cgrid(unsigned((p.N + 63) / 64), unsigned((p.K + 255) / 256), unsigned(nb));
+        hipLaunchKernelGGL(tg::tg_class_cols, cgrid, dim3(256), 0, st, B + z0 * p.sB, p.K, p.N, p.sB,
+                           clsB + z0 * p.N);
+        TG_HIP(hipGetLastError());
+        dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+        hipLaunchKernelGGL((tg::tg_transpose<double>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB,
+                           BT + z0 * p.K * p.N, p.K, p.N, p.sB, p.K * p.N);
+        TG_HIP(hipGetLastError());
+    }
+    KernelTimer timer(st);
+    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+        const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+        hipLaunchKernelGGL((tg::tg_gemm_dl64<SR>), dim3(unsigned(tiles_m * tiles_n), 1, unsigned(nb)),
+                           dim3(256), Cfg::LDS_BYTES, st, A + z0 * p.sA, B + z0 * p.sB,
+                           BT + z0 * p.K * p.N, static_cast<double*>(p.C) + z0 * p.sC,
+                           p.IDX + z0 * p.sC, clsA + z0 * p.M, clsB + z0 * p.N, p.M, p.N, p.K,
+                           p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+        TG_HIP(hipGetLastError());
+    }
+    return TG_OK;
 }
 
 // Direct-to-LDS kernel for 32-bit types (partial edge tiles allowed, see
@@ -483,7 +543,7 @@ constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
 // The kernel a problem runs on.
-enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, TILES_EXACT, TILES_CHUNKED, TILES };
+enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, DL64, TILES_EXACT, TILES_CHUNKED, TILES };
 
 struct Plan {
     Path path = Path::TILES;
@@ -499,7 +559,8 @@ bool uses_workspace(const Plan& pl, bool argmax) {
         case Path::KRES:
         case Path::TILES_EXACT:
         case Path::TILES: return false;
-        case Path::TILES_CHUNKED: return true;
+        case Path::TILES_CHUNKED:
+        case Path::DL64: return true;
         default: return argmax || pl.splits > 1;
     }
 }
@@ -594,6 +655,18 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             pl.splits = 1;
         }
     }
+    if constexpr (std::is_same<T, double>::value) {
+        // f64 argmax beyond the exact range on at least one round of
+        // 64 x 128 tiles, with the workspace for B^T and the operand classes.
+        const int64_t tiles = ((p.M + tg::Dl64Cfg::BM - 1) / tg::Dl64Cfg::BM) *
+                              ((p.N + tg::Dl64Cfg::BN - 1) / tg::Dl64Cfg::BN) * p.batch;
+        if (argmax && !exact && p.K > exact_tiles_max_k<T>() && tiles >= 256 &&
+            tg::dl64_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX) &&
+            dl64_ws_bytes(p.batch, p.M, p.N, p.K) <= ws_bytes) {
+            pl.path = Path::DL64;
+            return pl;
+        }
+    }
     if (!argmax)
         pl.path = Path::TILES;
     else if (exact || p.K <= exact_tiles_max_k<T>())
@@ -607,6 +680,9 @@ template <int SR, typename T>
 int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) {
     const Plan pl = plan_typed<SR, T>(p, ws_bytes);
     if (pl.path == Path::SHORTK) return run_gemm_shortk<SR, T>(p, st);
+    if constexpr (std::is_same<T, double>::value) {
+        if (pl.path == Path::DL64) return run_gemm_dl64<SR>(p, ws, st);
+    }
     if constexpr (sizeof(T) == 4) {
         switch (pl.path) {
             case Path::KRES8:
@@ -732,6 +808,7 @@ const char* path_name(Path path) {
         case Path::DL_44_8: return "dl_4x4_cl8";
         case Path::DL_44_16: return "dl_4x4_cl16";
         case Path::DL_44_32: return "dl_4x4_cl32";
+        case Path::DL64: return "dl64_4x8_cl16";
         case Path::TILES_EXACT: return "tiles_exact";
         case Path::TILES_CHUNKED: return "tiles_chunked";
         case Path::TILES: return "tiles";
@@ -767,6 +844,8 @@ size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int
                            bool with_argmax) {
     if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
     size_t w = bt_bytes_for(dt, batch, m, n, k, with_argmax);
+    if (dt == TG_F64 && with_argmax)  // operand classes of the f64 direct-to-LDS kernel
+        w += round_up(size_t(batch) * size_t(m + n) * 4, 256);
     if (elem_size(dt) == 4) {
         const int s1 = tg::dl_splits(m, n, k, batch), s2 = tg::dl_splits(n, m, k, batch);
         const int s = s1 > s2 ? s1 : s2;
