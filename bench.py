@@ -60,7 +60,7 @@ WORKLOAD_NAMES = {
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
-    "C1": "tg_gemm_dl<MaxPlus, f32, argmax> split-K x4 + tg_merge_splits",
+    "C1": "tg_gemm_dl<MaxPlus, f32, argmax> split-K x2 + tg_merge_splits",
     "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
     "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",

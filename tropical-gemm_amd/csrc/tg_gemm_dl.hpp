@@ -112,15 +112,18 @@ inline bool dl_full_tiles(int64_t M, int64_t N, int64_t K) {
 }
 
 // Split K for problems with too few 64 x 64 tiles (partial ones included) to
-// fill the chip: the largest power of two S with at most 1024 workgroups in
-// total, slices of at least 256 k and slice lengths that are multiples of 64.
+// fill the chip: the largest power of two S with at most 512 workgroups in
+// total (two per CU: longer slices, each resolving its own argmax, beat four
+// per CU; MaxPlus f32 1024^3 + argmax on MI355X: S = 2 69 us against 77 us
+// for S = 4 and 95 us for S = 8), slices of at least 256 k and slice
+// lengths that are multiples of 64.
 // N a multiple of 4, as the kernel needs (the merge then reads whole 16-byte
 // groups of the dense M x N partials).
 inline int dl_splits(int64_t M, int64_t N, int64_t K, int64_t batch) {
     if (M <= 0 || N <= 0 || N % 4 != 0 || K % 64 != 0 || batch <= 0) return 1;
     const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64) * batch;
     int s = 1;
-    while (tiles * s * 2 <= 1024 && K % (int64_t(64) * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
+    while (tiles * s * 2 <= 512 && K % (int64_t(64) * s * 2) == 0 && K / (s * 2) >= 256) s *= 2;
     return s;
 }
 
