@@ -24,12 +24,15 @@
 //     memory (K too large for LDS) the mask comes from 64-bit ballots over
 //     the bits of the bin index instead (wave_match_mask).
 //   * Summing (group_sum): in passes of kStageRanks ranks, each member of
-//     rank r0 + u posts its value to row u, column leader, of a per-wave LDS
-//     stage, and every leader reads its column: kStageRanks values, the
-//     missing ranks +0.0.  Adding +0.0 never changes a running sum that
-//     starts from +0.0 (such a sum is never -0.0 under round-to-nearest), so
-//     the leader adds every row unconditionally.  Readers clear their column
-//     behind them, so the stage is all +0.0 between passes.
+//     rank r0 + u posts its value to slot u of its leader's kStageRanks
+//     contiguous slots in a per-wave LDS stage, and each leader whose group
+//     reaches rank r0 reads its slots with one vector load: kStageRanks
+//     values, the missing ranks +0.0.  Adding +0.0 never changes a running
+//     sum that starts from +0.0 (such a sum is never -0.0 under
+//     round-to-nearest), so the leader adds every slot unconditionally.  It
+//     clears its slots behind it, so the stage is all +0.0 between passes;
+//     no other lane touches the stage, which keeps the LDS work of a pass
+//     proportional to the groups that need it.
 //
 #pragma once
 
@@ -73,50 +76,54 @@ __device__ __forceinline__ void lds_or(U* p, U v) {
 
 // Groups the active lanes by LDS bin (see the header comment): returns the
 // mask of the active lanes whose key equals this lane's (0 when inactive)
-// and the bin's value before this block in `before`.  Leaves garbage in the
-// touched bins: the leaders overwrite them (lds_apply).
+// and the bin's value before this block in `before`.  Inactive lanes run the
+// same steps on their own dummy slot, so no step needs an exec mask.  Leaves
+// garbage in the touched bins: the leaders overwrite them (lds_apply).
 template <typename T>
-__device__ __forceinline__ uint64_t lds_group(T* bins, int32_t key, bool active, T& before) {
+__device__ __forceinline__ uint64_t lds_group(T* bins, T* dummy, int32_t key, bool active,
+                                              T& before) {
     const int lane = threadIdx.x & 63;
-    uint64_t m = 0;
-    before = T(0);
+    T* const target = active ? bins + key : dummy + lane;
     if constexpr (sizeof(T) == 8) {
-        uint64_t* slot = reinterpret_cast<uint64_t*>(bins) + (active ? key : 0);
-        if (active) {
-            before = __builtin_bit_cast(T, lds_ld(slot));
-            lds_st(slot, uint64_t(0));
-            lds_or(slot, uint64_t(1) << lane);
-            m = lds_ld(slot);
-        }
+        uint64_t* slot = reinterpret_cast<uint64_t*>(target);
+        before = __builtin_bit_cast(T, lds_ld(slot));
+        lds_st(slot, uint64_t(0));
+        lds_or(slot, uint64_t(1) << lane);
+        const uint64_t m = lds_ld(slot);
+        return active ? m : 0;
     } else {
-        uint32_t* slot = reinterpret_cast<uint32_t*>(bins) + (active ? key : 0);
-        uint32_t lo = 0, hi = 0;
-        if (active) {
-            before = __builtin_bit_cast(T, lds_ld(slot));
-            lds_st(slot, 0u);
-        }
-        if (active && lane < 32) lds_or(slot, 1u << lane);
-        if (active) {
-            lo = lds_ld(slot);
-            lds_st(slot, 0u);
-        }
-        if (active && lane >= 32) lds_or(slot, 1u << (lane - 32));
-        if (active) hi = lds_ld(slot);
-        m = (uint64_t(hi) << 32) | lo;
+        // Each half of the wave ORs its bits in turn; the other half ORs into
+        // its own dummy slot meanwhile (atomics on one address serialize).
+        uint32_t* slot = reinterpret_cast<uint32_t*>(target);
+        uint32_t* spare = reinterpret_cast<uint32_t*>(dummy + lane);
+        const uint32_t bit = 1u << (lane & 31);
+        before = __builtin_bit_cast(T, lds_ld(slot));
+        lds_st(slot, 0u);
+        lds_or(lane < 32 ? slot : spare, bit);
+        const uint32_t lo = lds_ld(slot);
+        lds_st(slot, 0u);
+        lds_or(lane < 32 ? spare : slot, bit);
+        const uint32_t hi = lds_ld(slot);
+        return active ? (uint64_t(hi) << 32) | lo : 0;
     }
-    return m;
 }
 
-// Ranks per stage pass, and the stage's size per wave in elements.
+// Ranks per stage pass.  A wave's stage: 64 leaders x kStageRanks slots,
+// then 64 dummy slots, one per lane (the targets of inactive lanes and of
+// non-leaders, so the grouping and the apply run without exec masks).
 constexpr int kStageRanks = 4;
-constexpr int kStageElems = kStageRanks * 64;
+constexpr int kStageSlots = kStageRanks * 64;
+constexpr int kStageElems = kStageSlots + 64;
 
 // The leader's sum before + g(leader) + g(rank 1) + g(rank 2) + ... of its
 // group (m: this lane's group mask, 0 when inactive); meaningful on leaders
-// only.  stage: this wave's kStageElems elements, all +0.0 on entry and on
+// only.  stage: this wave's kStageSlots slots, all +0.0 on entry and on
 // return.  Wave-uniform: call with the whole wave active.
+// Stage: 64 leaders x kStageRanks contiguous slots; 16-byte aligned (the
+// kernels put the stages at the start of their LDS).
 template <typename T>
 __device__ __forceinline__ T group_sum(uint64_t m, T g, T before, bool& leader, T* stage) {
+    typedef T Slots __attribute__((ext_vector_type(kStageRanks)));
     const int lane = threadIdx.x & 63;
     const uint32_t rank =
         __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
@@ -125,37 +132,45 @@ __device__ __forceinline__ T group_sum(uint64_t m, T g, T before, bool& leader, 
     T acc = before + g;
     if (__ballot(leader && size > 1)) {
         const int lead = m != 0 ? int(__builtin_ctzll(m)) : 0;
+        Slots* mine = reinterpret_cast<Slots*>(stage) + lane;
         for (int r0 = 1; __ballot(leader && size > r0); r0 += kStageRanks) {
             const uint32_t d = rank - uint32_t(r0);
-            if (m != 0 && d < uint32_t(kStageRanks)) lds_st(stage + d * 64 + lead, g);
-            T v[kStageRanks];
+            if (m != 0 && d < uint32_t(kStageRanks)) stage[lead * kStageRanks + int(d)] = g;
+            // The members' stores are issued before the leaders' loads (LDS
+            // executes a wave's instructions in order); the compiler must
+            // not move them across, as it cannot see the other lanes.
+            asm volatile("" ::: "memory");
+            if (leader && size > r0) {
+                const Slots v = *mine;
+                *mine = Slots(T(0));
 #pragma unroll
-            for (int u = 0; u < kStageRanks; ++u) v[u] = lds_ld(stage + u * 64 + lane);
-#pragma unroll
-            for (int u = 0; u < kStageRanks; ++u) lds_st(stage + u * 64 + lane, T(0));
-#pragma unroll
-            for (int u = 0; u < kStageRanks; ++u) acc = acc + v[u];
+                for (int u = 0; u < kStageRanks; ++u) acc = acc + v[u];
+            }
+            asm volatile("" ::: "memory");
         }
     }
     return acc;
 }
 
-// Zeroes this wave's stage.
+// Zeroes the slots of this wave's stage.
 template <typename T>
 __device__ __forceinline__ void stage_clear(T* stage) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int u = 0; u < kStageRanks; ++u) lds_st(stage + u * 64 + lane, T(0));
+    for (int u = 0; u < kStageRanks; ++u) stage[u * 64 + lane] = T(0);
+    asm volatile("" ::: "memory");
 }
 
 // bins[key] += g in lane order among equal keys, bins in LDS.  Wave-uniform.
 template <typename T>
 __device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active) {
+    const int lane = threadIdx.x & 63;
+    T* const dummy = stage + kStageSlots;
     T before;
-    const uint64_t m = lds_group(bins, key, active, before);
+    const uint64_t m = lds_group(bins, dummy, key, active, before);
     bool leader;
     const T acc = group_sum(m, g, before, leader, stage);
-    if (leader) lds_st(reinterpret_cast<T*>(bins) + key, acc);
+    lds_st(leader ? bins + key : dummy + lane, acc);
 }
 
 // bins[key * es] += g in lane order among equal keys, bins in global memory
@@ -184,8 +199,8 @@ __device__ __forceinline__ void global_apply(T* bins, T* stage, int64_t es, int3
 
 // ---------------------------------------------------------------------------
 // grad_A.  rows = batch * M; row rr is (z = rr / M, i = rr % M).  Each wave
-// owns one row at a time; LDS: K bins per wave (not with GLOBAL), then a
-// stage of kStageElems per wave: waves * (K + kStageElems) * sizeof(T).
+// owns one row at a time; LDS: a stage of kStageElems per wave, then K bins
+// per wave (not with GLOBAL): waves * (kStageElems + K) * sizeof(T).
 //   MULT: MaxMul rule, g *= B[z][k][j] (OTHER = B, row-major K x N).
 // GLOBAL: the bins are the grad_A row itself (K too large for LDS).
 // grid: any size (grid-stride over rows), block = 64 * waves.
@@ -202,8 +217,8 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
     const int waves = blockDim.x >> 6;
     const int nbits = key_bits(K);
     constexpr int PF = 8;  // blocks of 64 contributions per prefetch chunk
-    const int64_t bins_elems = GLOBAL ? 0 : int64_t(waves) * K;
-    T* stage = reinterpret_cast<T*>(bwd_lds) + bins_elems + int64_t(wave) * kStageElems;
+    T* stage = reinterpret_cast<T*>(bwd_lds) + int64_t(wave) * kStageElems;
+    T* row_bins = reinterpret_cast<T*>(bwd_lds) + int64_t(waves) * kStageElems + int64_t(wave) * K;
     stage_clear(stage);
     for (int64_t rr = int64_t(blockIdx.x) * waves + wave; rr < rows;
          rr += int64_t(gridDim.x) * waves) {
@@ -212,7 +227,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
         const int32_t* k_row = IDX + z * sC + i * N;
         const T* other = MULT ? OTHER + z * sO : nullptr;
         T* out = GA + z * sA + i * K;
-        T* bins = GLOBAL ? out : reinterpret_cast<T*>(bwd_lds) + int64_t(wave) * K;
+        T* bins = GLOBAL ? out : row_bins;
         if constexpr (GLOBAL) {
             for (int64_t k = lane; k < K; k += 64)
                 __hip_atomic_store(bins + k, T(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -280,8 +295,8 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
 // column groups, so the W-column segments that share a cache line are read
 // and written through one L2.
 //   MULT: MaxMul rule, g *= A[z][i][k] (OTHER = A, row-major M x K).
-// LDS: W * K bins (not with GLOBAL), the tile, kBwdTileRows (W + 1) (4 +
-// sizeof(T)) bytes, then a stage of kStageElems per wave.
+// LDS: a stage of kStageElems per wave, W * K bins (not with GLOBAL), then
+// the tile, kBwdTileRows (W + 1) (4 + sizeof(T)) bytes.
 // grid: any size (grid-stride over column groups), block = 64 * W, W <= 8.
 // ---------------------------------------------------------------------------
 constexpr int kBwdTileRows = 256;
@@ -300,14 +315,13 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
     const int W = blockDim.x >> 6;
     const int stride = W + 1;
     const int nbits = key_bits(K);
-    T* bins_all = reinterpret_cast<T*>(bwd_lds);
+    T* stage = reinterpret_cast<T*>(bwd_lds) + wave * kStageElems;
+    unsigned char* const after_stage = bwd_lds + size_t(W) * kStageElems * sizeof(T);
+    T* bins_all = reinterpret_cast<T*>(after_stage);
     const int64_t bins_bytes = GLOBAL ? 0 : int64_t(W) * K * int64_t(sizeof(T));
-    T* tile_g = reinterpret_cast<T*>(bwd_lds + bins_bytes);
+    T* tile_g = reinterpret_cast<T*>(after_stage + bins_bytes);
     int32_t* tile_k =
-        reinterpret_cast<int32_t*>(bwd_lds + bins_bytes + kBwdTileRows * stride * sizeof(T));
-    T* stage = reinterpret_cast<T*>(bwd_lds + bins_bytes +
-                                    kBwdTileRows * stride * (sizeof(T) + 4)) +
-               wave * kStageElems;
+        reinterpret_cast<int32_t*>(after_stage + bins_bytes + kBwdTileRows * stride * sizeof(T));
     stage_clear(stage);
     // This thread's staging slots: rows sr + 64 t (t < TB), column sq.
     const int sr = tid / W, sq = tid - (tid / W) * W;
