@@ -395,11 +395,12 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
         if constexpr (!GLOBAL) {
             __syncthreads();  // every wave's bins are complete
             // The W columns leave together: row k of the group is W
-            // consecutive elements of grad_B.
-            for (int64_t e = tid; e < int64_t(W) * K; e += blockDim.x) {
-                const int64_t k = e / W;
-                const int q = int(e - k * W);
-                if (c0 + q < N) outz[k * N + c0 + q] = bins_all[int64_t(q) * K + k];
+            // consecutive elements of grad_B.  blockDim = 64 W, so thread tid
+            // writes column q = tid % W of rows tid / W, + 64, + 128, ...
+            if (c0 + sq < N) {
+                const T* src = bins_all + int64_t(sq) * K;
+                T* dst = outz + c0 + sq;
+                for (int64_t k = sr; k < K; k += 64) dst[k * N] = src[k];
             }
         }
         __syncthreads();  // the next group zeroes the bins and restages
