@@ -12,6 +12,12 @@
 //                     three-input f64 max on gfx950)
 // Grid: 256 workgroups x waves_per_simd of 256 threads (4 waves, one per
 // SIMD), so waves/SIMD = 1, 2, 4 or 8 across the sweep.
+//
+// A second probe times LDS reads alone (ds_read_b128, eight independent
+// reads per iteration, 32 KB of LDS per workgroup): every lane reading its
+// own 16 bytes (1 KB per instruction), and the fragment pattern of the
+// tiled kernels' B reads, where the 64 lanes of a wave read 16 distinct
+// 16-byte vectors (256 B per instruction, each delivered to 4 lanes).
 // Build: make -C tropical-gemm_amd probe; run: tropical-gemm_amd/probe/tg_issue_probe
 #include <hip/hip_runtime.h>
 
@@ -74,6 +80,57 @@ __global__ __launch_bounds__(256) void chains(const T* __restrict__ a_in, const 
     out[blockIdx.x * 256 + threadIdx.x] = s;
 }
 
+// LDS read throughput: lane l of a wave reads vector (l % DISTINCT) of its
+// wave's window; the window moves every iteration.
+template <int DISTINCT>
+__global__ __launch_bounds__(256) void lds_reads(unsigned* __restrict__ out, int iters) {
+    __shared__ __align__(16) uint4 buf[2048];  // 32 KB
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 2048; i += 256) buf[i] = make_uint4(i, 3 * i, 5 * i, 7 * i);
+    __syncthreads();
+    const int wave = tid >> 6, lane = tid & 63;
+    int base = wave * 64 + lane % DISTINCT;
+    uint4 keep = make_uint4(0, 0, 0, 0);
+    for (int it = 0; it < iters; ++it) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = buf[(base + u * 256) & 2047];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) asm volatile("" ::"v"(v[u].x), "v"(v[u].y), "v"(v[u].z), "v"(v[u].w));
+        keep.x ^= v[0].x;
+        base += 17;
+    }
+    out[blockIdx.x * 256 + tid] = keep.x;
+}
+
+template <int DISTINCT>
+void run_lds(const char* name, int wgs_per_cu, int iters) {
+    unsigned* o;
+    const int blocks = 256 * wgs_per_cu;
+    CK(hipMalloc(&o, size_t(blocks) * 256 * sizeof(unsigned)));
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    for (int w = 0; w < 3; ++w) hipLaunchKernelGGL((lds_reads<DISTINCT>), dim3(blocks), dim3(256), 0, 0, o, iters);
+    CK(hipGetLastError());
+    CK(hipEventRecord(e0));
+    const int reps = 5;
+    for (int w = 0; w < reps; ++w) hipLaunchKernelGGL((lds_reads<DISTINCT>), dim3(blocks), dim3(256), 0, 0, o, iters);
+    CK(hipEventRecord(e1));
+    CK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CK(hipEventElapsedTime(&ms, e0, e1));
+    ms /= reps;
+    const double instr = double(blocks) * 4 * iters * 8;  // wave instructions
+    std::printf("%-28s wgs/CU=%d  %.3f ms  %5.3f wave-reads/ns per CU  %6.1f B/ns per CU delivered  %6.1f B/ns per CU distinct\n",
+                name, wgs_per_cu, ms, instr / ms / 1e6 / 256, instr * 1024 / ms / 1e6 / 256,
+                instr * 16 * DISTINCT / ms / 1e6 / 256);
+    std::fflush(stdout);
+    CK(hipFree(o));
+    CK(hipEventDestroy(e0));
+    CK(hipEventDestroy(e1));
+}
+
 template <typename T, int MIX>
 void run(const char* name, int wps, int iters, int instr_per_iter) {
     T *a, *b, *o;
@@ -118,6 +175,10 @@ int main() {
         run<float, F32_IEEE>("f32 add+maximum3, A in VGPR", wps, iters, 64 + 32 + 8);
         run<float, F32_SGPR>("f32 add+max3, A in SGPR", wps, iters, 64 + 32 + 8);
         run<double, F64_VGPR>("f64 add+max, A in VGPR", wps, iters, 64 + 64 + 8);
+    }
+    for (int w = 1; w <= 4; ++w) {
+        run_lds<64>("LDS b128, 64 distinct/wave", w, 4000);
+        run_lds<16>("LDS b128, 16 distinct/wave", w, 4000);
     }
     return 0;
 }
