@@ -141,17 +141,23 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     // the loads classify every in-bounds operand (one v_cmp_class each into
     // wave masks), and a tile whose operands could make a NaN product is
     // recomputed with the reference's serial rule in the epilogue.
+    // The wave's findings are bits of one wave-uniform word (A: nan, c1, c2
+    // at bits 0-2; B at 3-5): one combined class test per operand, and the
+    // three separate ones only when the wave holds a special value (64-bit
+    // ballot masks per class kept the SGPRs busy enough to spill).
     constexpr bool CHECK = std::is_same<T, double>::value && !EXACT;
     constexpr int CLS1 = SR == SR_MAXMUL ? 516 : 512;  // +-inf | +inf
     constexpr int CLS2 = SR == SR_MAXMUL ? 96 : 4;     // +-0   | -inf
-    uint64_t fl[6] = {0, 0, 0, 0, 0, 0};  // A: nan, c1, c2; B: nan, c1, c2
+    uint32_t fl = 0;
     __shared__ int danger_flags;
     if (CHECK && tid == 0) danger_flags = 0;
     auto classify = [&](bool inb, T x, int o) {
         if constexpr (CHECK) {
-            fl[o] |= __ballot(inb && __builtin_amdgcn_class(x, 3));
-            fl[o + 1] |= __ballot(inb && __builtin_amdgcn_class(x, CLS1));
-            fl[o + 2] |= __ballot(inb && __builtin_amdgcn_class(x, CLS2));
+            if (__any(inb && __builtin_amdgcn_class(x, 3 | CLS1 | CLS2))) {
+                fl |= (__any(inb && __builtin_amdgcn_class(x, 3)) ? 1u : 0u) << o;
+                fl |= (__any(inb && __builtin_amdgcn_class(x, CLS1)) ? 2u : 0u) << o;
+                fl |= (__any(inb && __builtin_amdgcn_class(x, CLS2)) ? 4u : 0u) << o;
+            }
         }
     };
     Vec16<T> ra[NVA], rb[NVB];
@@ -372,8 +378,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     // output of an f64 tile whose operands could make one (CHECK above).
     bool danger = false;
     if constexpr (CHECK) {
-        const int w = (fl[0] != 0) | (fl[1] != 0) << 1 | (fl[2] != 0) << 2 | (fl[3] != 0) << 3 |
-                      (fl[4] != 0) << 4 | (fl[5] != 0) << 5;
+        const int w = int(fl);
         if ((tid & 63) == 0 && w != 0) atomicOr(&danger_flags, w);
         __syncthreads();
         const int f = danger_flags;
