@@ -121,10 +121,10 @@ int tg_gemm(int device, tg_semiring semiring, tg_dtype dtype, tg_layout layout,
 /* Bytes of device workspace tg_gemm_ws needs for this problem, each part
  * 256-byte aligned: with argmax, B^T staging of batch x k x max(m, n)
  * elements (column-major calls swap the operands, so the bound covers both
- * layouts) and, for f64, 4 bytes per row of A and column of B (operand
- * classes of the f64 direct-to-LDS kernel); for 32-bit problems the library
- * splits in k, the per-slice partials (values, and indices with argmax).
- * 0 for value-only problems that are not split.  batch = 1 for single
+ * layouts); for f64, 4 bytes per row of A and column of B (operand classes
+ * of the f64 direct-to-LDS kernel); for 32-bit problems the library splits
+ * in k, the per-slice partials (values, and indices with argmax).  0 for
+ * 32-bit value-only problems that are not split.  batch = 1 for single
  * products. */
 size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,
                               int with_argmax);

@@ -131,6 +131,8 @@ def test_python_layer_rejects_host_tensors():
     ("maxplus", "f32", 67, 45, 40, True, "tiles_exact"),
     ("maxplus", "f64", 4096, 4096, 4096, True, "dl64_4x8_cl16"),
     ("maxplus", "f64", 64, 64, 640, True, "tiles_chunked"),
+    ("maxplus", "f64", 4096, 4096, 4096, False, "dl64_4x8"),
+    ("maxplus", "f64", 4096, 4096, 128, False, "tiles"),
 ])
 def test_gemm_plan_names_the_configured_paths(sr, dt, m, n, k, argmax, expected):
     if expected == "shortk":

@@ -1,11 +1,11 @@
-"""f64 direct-to-LDS argmax kernel (tg_gemm_dl64).
+"""f64 direct-to-LDS kernel (tg_gemm_dl64), with and without argmax.
 
-Large f64 argmax problems run on it when the workspace holds B^T and the
-operand classes (tg_gemm_workspace_size); a workspace of only the B^T
-minimum runs the same product on the generic chunked kernel.  Both must give
-the same bits and argmax, equal to the oracle on sampled rows; NaN products
-(NaN operands, +inf meeting -inf, 0 * inf) follow the reference's serial
-rule through the class prepass and the serial rerun.
+Large f64 problems run on it when the workspace holds the operand classes
+(and B^T with argmax; tg_gemm_workspace_size); a workspace of only the B^T
+minimum (argmax) or none (value-only) runs the same product on the generic
+kernel.  Both must give the same bits (and argmax), equal to the oracle on
+sampled rows; NaN products (NaN operands, +inf meeting -inf, 0 * inf) follow
+the reference's serial rule through the class prepass and the serial rerun.
 """
 import ctypes
 
@@ -22,27 +22,30 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _run(sr, a, b, full_ws):
+def _run(sr, a, b, full_ws, argmax=True):
     from tropical_gemm import _native as nat
 
     lib = nat.load()
     m, k = a.shape
     n = b.shape[1]
-    ws_bytes = (lib.tg_gemm_workspace_size(nat.DTYPE["f64"], 1, m, n, k, 1) if full_ws
-                else -(-(k * max(m, n) * 8) // 256) * 256)
-    plan = nat.gemm_plan(sr, "f64", m, n, k, True, workspace_bytes=ws_bytes)
+    if full_ws:
+        ws_bytes = lib.tg_gemm_workspace_size(nat.DTYPE["f64"], 1, m, n, k, int(argmax))
+    else:
+        ws_bytes = -(-(k * max(m, n) * 8) // 256) * 256 if argmax else 0
+    plan = nat.gemm_plan(sr, "f64", m, n, k, argmax, workspace_bytes=ws_bytes)
     ta = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     tb = torch.from_numpy(np.ascontiguousarray(b)).to(DEV)
     c = torch.empty(m * n, dtype=torch.float64, device=DEV)
-    am = torch.empty(m * n, dtype=torch.int32, device=DEV)
+    am = torch.empty(m * n, dtype=torch.int32, device=DEV) if argmax else None
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=DEV)
-    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    print(f"[case] dl64 {sr} {m}x{n}x{k} {plan}", flush=True)
+    print(f"[case] dl64 {sr} {m}x{n}x{k} argmax={argmax} {plan}", flush=True)
     nat.check(lib.tg_gemm_ws(0, nat.SEMIRING[sr], nat.DTYPE["f64"], 0, p(ta), p(tb), p(c), p(am),
                              m, n, k, p(ws), ws_bytes, stream))
     torch.cuda.synchronize()
-    return plan, c.cpu().numpy().reshape(m, n), am.cpu().numpy().reshape(m, n)
+    return (plan, c.cpu().numpy().reshape(m, n),
+            am.cpu().numpy().reshape(m, n) if argmax else None)
 
 
 def _check(c, am, c_ref, am_ref):
@@ -90,3 +93,43 @@ def test_dl64_nan_rule(sr):
     c_ref, am_ref = oracle.gemm(sr, a[rows], b)
     assert np.isnan(c_ref).any()
     _check(c[rows], am[rows], c_ref, am_ref)
+
+
+def _check_values(c, c_ref):
+    nan = np.isnan(c_ref)
+    np.testing.assert_array_equal(np.isnan(c), nan)
+    np.testing.assert_array_equal(tc.bits(c[~nan]), tc.bits(c_ref[~nan]))
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+@pytest.mark.parametrize("m,n,k", [(1024, 4096, 640), (1000, 4092, 672)])
+def test_dl64_value_only_matches_generic_and_oracle(sr, m, n, k):
+    """Value-only on the f64 direct-to-LDS kernel: the same bits as the
+    generic kernel (run by the same call without a workspace) and the
+    oracle's values on sampled rows.  The data has no zeros, so no +-0 tie
+    makes the sign of a value-only maximum open."""
+    a, b = _operands(sr, m, n, k, seed=3 * m + k)
+    if sr != "maxmul":
+        a[a == 0] = 0.125
+        b[b == 0] = -0.125
+    plan, c, _ = _run(sr, a, b, full_ws=True, argmax=False)
+    assert plan == "dl64_4x8"
+    plan0, c0, _ = _run(sr, a, b, full_ws=False, argmax=False)
+    assert plan0 == "tiles"
+    _check_values(c, c0)
+    rows = np.array([0, 1, 63, 64, 500, m - 1])
+    c_ref, _ = oracle.gemm(sr, a[rows], b)
+    _check_values(c[rows], c_ref)
+
+
+@pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
+def test_dl64_value_only_nan_rule(sr):
+    m, n, k = 1024, 4096, 640
+    a, b = nan_inputs(sr, np.float64, m, n, k, seed=23)
+    plan, c, _ = _run(sr, a, b, full_ws=True, argmax=False)
+    assert plan == "dl64_4x8"
+    special = ~np.isfinite(a).all(axis=1) | (a == 0).any(axis=1)
+    rows = np.unique(np.concatenate([np.nonzero(special)[0], np.arange(0, m, 97), [m - 1]]))
+    c_ref, _ = oracle.gemm(sr, a[rows], b)
+    assert np.isnan(c_ref).any()
+    _check_values(c[rows], c_ref)

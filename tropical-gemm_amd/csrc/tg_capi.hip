@@ -199,15 +199,17 @@ WsLayout ws_layout(tg_dtype dt, int64_t batch, int64_t M, int64_t N, int64_t K, 
     return w;
 }
 
-// Workspace of the f64 direct-to-LDS argmax kernel: B^T (batch x K x N),
-// then the row classes of A (batch x M) and column classes of B (batch x N).
-size_t dl64_ws_bytes(int64_t batch, int64_t M, int64_t N, int64_t K) {
-    return round_up(size_t(batch) * size_t(K) * size_t(N) * 8, 256) +
+// Workspace of the f64 direct-to-LDS kernel: B^T (batch x K x N, argmax
+// only), then the row classes of A (batch x M) and column classes of B
+// (batch x N).
+size_t dl64_ws_bytes(int64_t batch, int64_t M, int64_t N, int64_t K, bool argmax) {
+    return (argmax ? round_up(size_t(batch) * size_t(K) * size_t(N) * 8, 256) : 0) +
            round_up(size_t(batch) * size_t(M + N) * 4, 256);
 }
 
-// f64 argmax, large problems (tg_gemm_dl64): B^T staging and the operand
-// class prepass, then the GEMM.  K % 32 == 0 and the rest of dl64_fits hold.
+// f64, large problems (tg_gemm_dl64): the operand class prepass and, with
+// argmax, B^T staging; then the GEMM.  K % 32 == 0 and the rest of dl64_fits
+// hold.
 template <int SR>
 int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
     using Cfg = tg::Dl64Cfg;
@@ -219,9 +221,11 @@ int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
         return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the staging grids");
     const double* A = static_cast<const double*>(p.A);
     const double* B = static_cast<const double*>(p.B);
+    const bool argmax = p.IDX != nullptr;
     unsigned char* wsb = static_cast<unsigned char*>(ws);
-    double* BT = reinterpret_cast<double*>(wsb);
-    uint32_t* cls = reinterpret_cast<uint32_t*>(wsb + round_up(size_t(p.batch) * size_t(p.K) * size_t(p.N) * 8, 256));
+    double* BT = argmax ? reinterpret_cast<double*>(wsb) : nullptr;
+    const size_t bt_bytes = argmax ? round_up(size_t(p.batch) * size_t(p.K) * size_t(p.N) * 8, 256) : 0;
+    uint32_t* cls = reinterpret_cast<uint32_t*>(wsb + bt_bytes);
     uint32_t* clsA = cls;
     uint32_t* clsB = cls + p.batch * p.M;
     hipLaunchKernelGGL(tg::tg_fill_zero, dim3(unsigned((p.batch * (p.M + p.N) * 4 / 16 + 255) / 256 + 1)),
@@ -240,19 +244,28 @@ int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
         hipLaunchKernelGGL(tg::tg_class_cols, cgrid, dim3(256), 0, st, B + z0 * p.sB, p.K, p.N, p.sB,
                            clsB + z0 * p.N);
         TG_HIP(hipGetLastError());
-        dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
-        hipLaunchKernelGGL((tg::tg_transpose<double>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB,
-                           BT + z0 * p.K * p.N, p.K, p.N, p.sB, p.K * p.N);
-        TG_HIP(hipGetLastError());
+        if (argmax) {
+            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
+            hipLaunchKernelGGL((tg::tg_transpose<double>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB,
+                               BT + z0 * p.K * p.N, p.K, p.N, p.sB, p.K * p.N);
+            TG_HIP(hipGetLastError());
+        }
     }
     KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
         const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
-        hipLaunchKernelGGL((tg::tg_gemm_dl64<SR>), dim3(unsigned(tiles_m * tiles_n), 1, unsigned(nb)),
-                           dim3(256), Cfg::LDS_BYTES, st, A + z0 * p.sA, B + z0 * p.sB,
-                           BT + z0 * p.K * p.N, static_cast<double*>(p.C) + z0 * p.sC,
-                           p.IDX + z0 * p.sC, clsA + z0 * p.M, clsB + z0 * p.N, p.M, p.N, p.K,
-                           p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+        const dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+        double* Cz = static_cast<double*>(p.C) + z0 * p.sC;
+        if (argmax)
+            hipLaunchKernelGGL((tg::tg_gemm_dl64<SR, true>), grid, dim3(256), Cfg::LDS_BYTES, st,
+                               A + z0 * p.sA, B + z0 * p.sB, BT + z0 * p.K * p.N, Cz,
+                               p.IDX + z0 * p.sC, clsA + z0 * p.M, clsB + z0 * p.N, p.M, p.N, p.K,
+                               p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n));
+        else
+            hipLaunchKernelGGL((tg::tg_gemm_dl64<SR, false>), grid, dim3(256), Cfg::TILE_BYTES, st,
+                               A + z0 * p.sA, B + z0 * p.sB, nullptr, Cz, nullptr, clsA + z0 * p.M,
+                               clsB + z0 * p.N, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                               int(tiles_n));
         TG_HIP(hipGetLastError());
     }
     return TG_OK;
@@ -543,7 +556,7 @@ constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
 // The kernel a problem runs on.
-enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, DL64, TILES_EXACT, TILES_CHUNKED, TILES };
+enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, DL64, DL64_VALUE, TILES_EXACT, TILES_CHUNKED, TILES };
 
 struct Plan {
     Path path = Path::TILES;
@@ -560,7 +573,8 @@ bool uses_workspace(const Plan& pl, bool argmax) {
         case Path::TILES_EXACT:
         case Path::TILES: return false;
         case Path::TILES_CHUNKED:
-        case Path::DL64: return true;
+        case Path::DL64:
+        case Path::DL64_VALUE: return true;
         default: return argmax || pl.splits > 1;
     }
 }
@@ -656,14 +670,17 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
         }
     }
     if constexpr (std::is_same<T, double>::value) {
-        // f64 argmax beyond the exact range on at least one round of
-        // 64 x 128 tiles, with the workspace for B^T and the operand classes.
+        // f64 on at least 256 tiles of 64 x 128 with the workspace for the
+        // operand classes (and B^T with argmax): argmax beyond the exact
+        // range, value-only from K = 256 (below that the class prepass and
+        // its launches weigh on the product).
         const int64_t tiles = ((p.M + tg::Dl64Cfg::BM - 1) / tg::Dl64Cfg::BM) *
                               ((p.N + tg::Dl64Cfg::BN - 1) / tg::Dl64Cfg::BN) * p.batch;
-        if (argmax && !exact && p.K > exact_tiles_max_k<T>() && tiles >= 256 &&
+        const bool deep = argmax ? !exact && p.K > exact_tiles_max_k<T>() : p.K >= 256;
+        if (deep && tiles >= 256 &&
             tg::dl64_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX) &&
-            dl64_ws_bytes(p.batch, p.M, p.N, p.K) <= ws_bytes) {
-            pl.path = Path::DL64;
+            dl64_ws_bytes(p.batch, p.M, p.N, p.K, argmax) <= ws_bytes) {
+            pl.path = argmax ? Path::DL64 : Path::DL64_VALUE;
             return pl;
         }
     }
@@ -681,7 +698,7 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
     const Plan pl = plan_typed<SR, T>(p, ws_bytes);
     if (pl.path == Path::SHORTK) return run_gemm_shortk<SR, T>(p, st);
     if constexpr (std::is_same<T, double>::value) {
-        if (pl.path == Path::DL64) return run_gemm_dl64<SR>(p, ws, st);
+        if (pl.path == Path::DL64 || pl.path == Path::DL64_VALUE) return run_gemm_dl64<SR>(p, ws, st);
     }
     if constexpr (sizeof(T) == 4) {
         switch (pl.path) {
@@ -809,6 +826,7 @@ const char* path_name(Path path) {
         case Path::DL_44_16: return "dl_4x4_cl16";
         case Path::DL_44_32: return "dl_4x4_cl32";
         case Path::DL64: return "dl64_4x8_cl16";
+        case Path::DL64_VALUE: return "dl64_4x8";
         case Path::TILES_EXACT: return "tiles_exact";
         case Path::TILES_CHUNKED: return "tiles_chunked";
         case Path::TILES: return "tiles";
@@ -844,7 +862,7 @@ size_t workspace_bytes_for(tg_dtype dt, int64_t batch, int64_t m, int64_t n, int
                            bool with_argmax) {
     if (batch <= 0 || m <= 0 || n <= 0 || k <= 0) return 0;
     size_t w = bt_bytes_for(dt, batch, m, n, k, with_argmax);
-    if (dt == TG_F64 && with_argmax)  // operand classes of the f64 direct-to-LDS kernel
+    if (dt == TG_F64)  // operand classes of the f64 direct-to-LDS kernel
         w += round_up(size_t(batch) * size_t(m + n) * 4, 256);
     if (elem_size(dt) == 4) {
         const int s1 = tg::dl_splits(m, n, k, batch), s2 = tg::dl_splits(n, m, k, batch);

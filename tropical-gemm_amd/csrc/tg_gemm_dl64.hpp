@@ -1,7 +1,7 @@
-// tg_gemm_dl64.hpp -- direct-to-LDS tropical GEMM with argmax for f64 (gfx950).
+// tg_gemm_dl64.hpp -- direct-to-LDS tropical GEMM for f64 (gfx950).
 //
-// Same contract as tg_gemm_tiles with argmax (tg_kernels.hpp), for large
-// f64 problems.  The byte layout is that of tg_gemm_dl's 64 x 128 tiles
+// Same contract as tg_gemm_tiles (tg_kernels.hpp), with or without argmax,
+// for large f64 problems.  The byte layout is that of tg_gemm_dl's 64 x 128 tiles
 // (tg_gemm_dl.hpp) with 8-byte elements: a 16-byte quad holds two k.
 //   A tile  64 rows x 16 k, 128-byte rows; quad q of row r stored at quad
 //           position q ^ ((r >> 2) & 7) (the four rows a wave reads at one k
@@ -12,8 +12,9 @@
 // columns (j >> 2) * 64 + tx*4 + (j & 3) (j < 8).  Per pair of k it reads 4
 // ds_read_b128 of A and 8 of B for 64 products: 3 bytes of LDS per product.
 // Per product one v_add_f64 and one v_max_f64 (v_min_f64): f64 has no
-// three-input max on gfx950.  About 210 VGPRs: two waves per SIMD, which the
-// issue probe measures at 92% of the f64 add+max ceiling.
+// three-input max on gfx950.  With argmax about 210 VGPRs: two waves per
+// SIMD, which the issue probe measures at 92% of the f64 add+max ceiling;
+// value-only (no chunk-start copies, no records) three.
 //
 // Argmax: one chunk per k-tile (CL = 16).  The running value alternates
 // between acc and alt from k-tile to k-tile, and a k-tile is recorded where
@@ -30,7 +31,8 @@
 // serial rule (cpu_select over the whole k range).
 //
 // Host-checked requirements (dl64_fits): K % 32 == 0 (k-tiles in pairs),
-// N % 4 == 0, 16-byte aligned A, B, C, IDX and batch strides multiples of 4;
+// N % 4 == 0, 16-byte aligned A, B, C, IDX (if any) and batch strides
+// multiples of 4;
 // chunk indices below 2^16.  Partial tiles in M and N: loads clamp into the
 // matrix, stores skip rows past M and 4-column groups past N.
 #pragma once
@@ -145,13 +147,14 @@ inline bool dl64_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, i
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     return M > 0 && N > 0 && K > 0 && K % 32 == 0 && N % 4 == 0 && K / Dl64Cfg::CL < 0xFFFF &&
            K < (int64_t(1) << 25) && N < (int64_t(1) << 27) && sA % 4 == 0 && sB % 4 == 0 &&
-           sC % 4 == 0 && a16(A) && a16(B) && a16(C) && IDX != nullptr && a16(IDX);
+           sC % 4 == 0 && a16(A) && a16(B) && a16(C) && (IDX == nullptr || a16(IDX));
 }
 
-// grid = (tiles_m * tiles_n, 1, batch), block = 256, LDS = Dl64Cfg::LDS_BYTES.
+// grid = (tiles_m * tiles_n, 1, batch), block = 256, LDS = Dl64Cfg::LDS_BYTES
+// (argmax) or Dl64Cfg::TILE_BYTES (value-only: BT and IDX unused).
 // clsA / clsB: row / column classes (batch x M, batch x N).
-template <int SR>
-__global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void tg_gemm_dl64(
+template <int SR, bool ARGMAX>
+__global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(ARGMAX ? 2 : 3))) void tg_gemm_dl64(
     const double* __restrict__ A, const double* __restrict__ B, const double* __restrict__ BT,
     double* __restrict__ C, int32_t* __restrict__ IDX, const uint32_t* __restrict__ clsA,
     const uint32_t* __restrict__ clsB, int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB,
@@ -178,8 +181,10 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     A += z * sA;
     B += z * sB;
     C += z * sC;
-    IDX += z * sC;
-    BT += z * (N * K);
+    if constexpr (ARGMAX) {
+        IDX += z * sC;
+        BT += z * (N * K);
+    }
     clsA += z * M;
     clsB += z * N;
     auto trow = [&](int i) { return ty * 4 + i; };
@@ -253,8 +258,21 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                 b[h][j + 1] = v.v[1];
             }
     };
+    // Value-only chains: v_max_f64 / v_min_f64 as written.  Through the
+    // compiler's maxnum the loop-carried value gets a canonicalizing max per
+    // k-tile, and the loop spilled; every operand here is an add result or a
+    // max of them, so it is canonical already.
+    auto join_f64 = [](T x, T y) {
+        T r;
+        if constexpr (SR == SR_MINPLUS)
+            asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+        else
+            asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+        return r;
+    };
     // The k-tile t (one chunk) in buffer buf: a chain from `from` into `to`,
-    // recorded where `to` strictly beats `from`.
+    // recorded where `to` strictly beats `from` (value-only: in place, no
+    // record).
     auto chunk = [&](int64_t t, int buf, const T (&from)[TM][TN], T (&to)[TM][TN]) {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 2) {
@@ -267,18 +285,23 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                     const T p0 = tmul<SR, T>(a[i][0], b[0][j]);
                     const T p1 = tmul<SR, T>(a[i][1], b[1][j]);
                     const T st = kk == 0 ? from[i][j] : to[i][j];
-                    to[i][j] = tjoin<SR, T>(tjoin<SR, T>(st, p0), p1);
+                    if constexpr (ARGMAX)
+                        to[i][j] = tjoin<SR, T>(tjoin<SR, T>(st, p0), p1);
+                    else
+                        to[i][j] = join_f64(join_f64(st, p0), p1);
                 }
         }
-        int32_t cv;
-        asm volatile("v_mov_b32 %0, %1" : "=v"(cv) : "s"(int32_t(t)));
+        if constexpr (ARGMAX) {
+            int32_t cv;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(cv) : "s"(int32_t(t)));
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; j += 4)
-                record4_f64<SR>(ch[i][j], ch[i][j + 1], ch[i][j + 2], ch[i][j + 3], to[i][j],
-                                to[i][j + 1], to[i][j + 2], to[i][j + 3], from[i][j],
-                                from[i][j + 1], from[i][j + 2], from[i][j + 3], cv);
+                for (int j = 0; j < TN; j += 4)
+                    record4_f64<SR>(ch[i][j], ch[i][j + 1], ch[i][j + 2], ch[i][j + 3], to[i][j],
+                                    to[i][j + 1], to[i][j + 2], to[i][j + 3], from[i][j],
+                                    from[i][j + 1], from[i][j + 2], from[i][j + 3], cv);
+        }
     };
 
     // k-tiles in pairs: the even one runs acc -> alt, the odd one alt -> acc.
@@ -292,7 +315,9 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
             __syncthreads();
             if (tt + 1 < nkt) issue_loads(tt + 1, h ^ 1);
             asm volatile("" : "+v"(swz_t));
-            if (h == 0)
+            if constexpr (!ARGMAX)
+                chunk(tt, h, acc, acc);
+            else if (h == 0)
                 chunk(tt, 0, acc, alt);
             else
                 chunk(tt, 1, alt, acc);
@@ -323,6 +348,43 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     // Outputs whose row and column could meet in a NaN product: recomputed
     // after the stores with the serial rule (one runtime loop over a mask).
     uint64_t redo = 0;
+    if constexpr (!ARGMAX) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int64_t gr = row0 + trow(i);
+            const uint32_t ra = clsA[gr < M ? gr : M - 1];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int64_t gc = col0 + tcol(j);
+                if (nan_danger<SR>(ra, clsB[gc < N ? gc : N - 1])) redo |= uint64_t(1) << (i * TN + j);
+            }
+            if (gr >= M) continue;
+#pragma unroll
+            for (int g = 0; g < TN / 4; ++g) {
+                const int64_t gc = col0 + g * 64 + tx * 4;
+                if (gc >= N) continue;  // N is a multiple of 4: whole groups only
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    Vec16<T> cv;
+                    cv.v[0] = acc[i][g * 4 + 2 * h];
+                    cv.v[1] = acc[i][g * 4 + 2 * h + 1];
+                    *reinterpret_cast<Vec16<T>*>(C + gr * N + gc + 2 * h) = cv;
+                }
+            }
+        }
+#pragma unroll 1
+        while (redo) {
+            const int o = __builtin_ctzll(redo);
+            redo &= redo - 1;
+            const int64_t gr = row0 + trow(o / TN), gc = col0 + tcol(o % TN);
+            if (gr >= M || gc >= N) continue;
+            T v;
+            int32_t ix;
+            cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
+            C[gr * N + gc] = v;
+        }
+        return;
+    }
     {
         uint32_t ra[TM], cb[TN];
 #pragma unroll
