@@ -11,7 +11,9 @@
  * tg_stream_synchronize() afterwards (the reference synchronises after every
  * launch, crates/tropical-gemm-cuda/src/kernels.rs:65).
  *
- * Semantics (bit-exact with the reference CPU path for non-NaN inputs):
+ * Semantics (bit-exact with the reference CPU path; a NaN product replaces
+ * the running value and the next product replaces a NaN, as the CPU's
+ * "keep acc iff acc >= p" rule does, types/max_plus.rs:66-73):
  *   C[i,j]      = (+)_k A[i,k] (x) B[k,j], k visited in ascending order;
  *   argmax[i,j] = the first k attaining C[i,j] (0 when no product beats the
  *                 tropical zero), written as int32 (the reference GPU's
