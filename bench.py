@@ -57,6 +57,7 @@ WORKLOAD_NAMES = {
     "C5": "C5: MaxPlus f32 4096^3 +argmax forward, then grad_A and grad_B backward",
     "M1": "M1: MaxPlus f32 65536x2048x8 +argmax (short K, HBM-bound)",
     "F1": "F1: MaxPlus f64 4096^3 +argmax",
+    "F2": "F2: MaxPlus f64 4096^3 value-only",
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
@@ -67,6 +68,7 @@ KERNEL_NAMES = {
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
     "F1": "tg_gemm_dl64<MaxPlus> (f64, 64x128 tiles, argmax)",
+    "F2": "tg_gemm_dl64<MaxPlus, value-only> (f64, 64x128 tiles)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
@@ -76,7 +78,7 @@ KERNEL_NAMES = {
 # launch; C1: the split GEMM launch (the merge adds 0.025e9).
 
 TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.052e9,
-           "C2": 1.775e9, "C3": 1.642e9, "F1": 3.438e9, "E1": 0.1435e9}
+           "C2": 1.775e9, "C3": 1.642e9, "F1": 3.438e9, "F2": 2.266e9, "E1": 0.1435e9}
 
 
 def cpu_model() -> str:
@@ -94,6 +96,9 @@ def cpu_model() -> str:
 # about 0.5-4 s of single-core work.  C1 and C4 run whole; M1's short K makes
 # the reference's blocked loops slow (0.07 GOP/s), hence its small slab.
 CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096, "F1": 256}
+# Configurations without a CPU restatement of the reference path they would
+# take (the reference's f64 value-only SIMD kernels are not restated).
+NO_CPU_BASELINE = {"F2": "no restatement of the reference's f64 value-only SIMD path"}
 
 
 def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> dict:
@@ -251,7 +256,7 @@ def main() -> int:
     # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--config", default="P",
-                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "E1"])
+                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "F2", "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of P's CPU-baseline slab (0 skips the CPU baseline of every "
                          "configuration)")
@@ -426,7 +431,9 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize(dev)
         out["copy_calibration_bytes"] = args.copy_mib << 20
-    if args.cpu_rows > 0:
+    if args.cpu_rows > 0 and args.config in NO_CPU_BASELINE:
+        out["cpu_baseline_note"] = NO_CPU_BASELINE[args.config]
+    elif args.cpu_rows > 0:
         rows = cpu_rows_for(args.config, args.cpu_rows)
         out["cpu_baseline"] = run_cpu_baseline(cfg, a, b, rows)
         out["gpu_vs_cpu_baseline"] = round(gops / out["cpu_baseline"]["value"], 1)

@@ -13,6 +13,7 @@ the host) to the CPU oracle.  Nothing here reads the reference.
     M1  MaxPlus f32 M=65536 K=8 N=2048 with argmax, N(0,1): short K, bound by
         HBM (the 0.5 GB output and argmax writes), not by the VALU
     F1  MaxPlus f64 4096^3 with argmax, A, B ~ N(0,1) (the f64 kernels)
+    F2  MaxPlus f64 4096^3 value-only, A, B ~ N(0,1)
     E1  tropical einsum "jik,lkj,lm->im", MaxPlus f32, N(0,1): i = l = m = 2048,
         j = 32, k = 64 (two 2048^3 contractions after two permutations)
 """
@@ -32,6 +33,7 @@ CONFIGS = {
                backward=True),
     "M1": dict(semiring="maxplus", dtype="f32", m=65536, k=8, n=2048, argmax=True, bound="hbm"),
     "F1": dict(semiring="maxplus", dtype="f64", m=4096, k=4096, n=4096, argmax=True),
+    "F2": dict(semiring="maxplus", dtype="f64", m=4096, k=4096, n=4096, argmax=False),
 }
 
 
@@ -49,7 +51,7 @@ def make_inputs(name: str, device="cuda", scale: float = 1.0):
     m = max(1, int(cfg["m"] * scale))
     k = cfg["k"] if name == "C4" else max(1, int(cfg["k"] * scale))
     n = cfg["n"] if name == "C4" else max(1, int(cfg["n"] * scale))
-    if name in ("P", "C1", "C5", "M1", "F1"):
+    if name in ("P", "C1", "C5", "M1", "F1", "F2"):
         dt = torch.float64 if cfg["dtype"] == "f64" else torch.float32
         a = torch.randn(m, k, generator=_gen(device, idx, 0), device=device, dtype=dt)
         b = torch.randn(k, n, generator=_gen(device, idx, 1), device=device, dtype=dt)
