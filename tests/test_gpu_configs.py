@@ -118,3 +118,21 @@ def test_c5_backward_full_size():
         np.add.at(s, idx, np.abs(g_np.astype(np.float64)))
         diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
         assert np.all(diff <= 4 * cnt * 2.0**-24 * s)
+
+
+@pytest.mark.parametrize("name,with_argmax,plan", [("F1", True, "dl64_4x8_cl16"),
+                                                   ("F2", False, "dl64_4x8")])
+def test_f64_configs_full_size(name, with_argmax, plan):
+    """F1 / F2 (f64 4096^3) at full size on the f64 direct-to-LDS kernel:
+    argmax consistency on every output (F1) and the oracle on sampled rows."""
+    from tropical_gemm import _native as nat
+
+    assert nat.gemm_plan("maxplus", "f64", 4096, 4096, 4096, with_argmax) == plan
+    cfg, a, b, c, am = _run(name, with_argmax)
+    if with_argmax:
+        _check_consistency(cfg["semiring"], a, b, c, am)
+    rows = np.array([0, 1, 2, 63, 64, 1000, 2047, 4095])
+    c_ref, am_ref = oracle.gemm(cfg["semiring"], a[rows].cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(tc.bits(c.cpu().numpy()[rows]), tc.bits(c_ref))
+    if with_argmax:
+        np.testing.assert_array_equal(am.cpu().numpy()[rows], am_ref.astype(np.int32))
