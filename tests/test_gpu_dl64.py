@@ -133,3 +133,56 @@ def test_dl64_value_only_nan_rule(sr):
     c_ref, _ = oracle.gemm(sr, a[rows], b)
     assert np.isnan(c_ref).any()
     _check_values(c[rows], c_ref)
+
+
+@pytest.mark.parametrize("argmax", [True, False])
+@pytest.mark.parametrize("sr", ["maxplus", "minplus"])
+def test_dl64_column_major(sr, argmax):
+    """Column-major calls run the row-major product C^T = B^T (x) A^T on the
+    same kernel (here M' = 4096, N' = 1024)."""
+    from tests.test_gpu_parity import gpu_gemm
+    from tropical_gemm import _native as nat
+
+    m, n, k = 1024, 4096, 640
+    plan = nat.gemm_plan(sr, "f64", m, n, k, argmax, layout="col")
+    assert plan == ("dl64_4x8_cl16" if argmax else "dl64_4x8")
+    a, b = _operands(sr, m, n, k, seed=91)
+    a[a == 0] = 0.125
+    b[b == 0] = -0.125
+    print(f"[case] dl64 col-major {sr} argmax={argmax}", flush=True)
+    c, am = gpu_gemm(sr, a, b, with_argmax=argmax, layout="col")
+    rows = np.array([0, 5, 511, m - 1])
+    c_ref, am_ref = oracle.gemm(sr, a[rows], b)
+    _check_values(c[rows], c_ref)
+    if argmax:
+        np.testing.assert_array_equal(am[rows].astype(np.int64), am_ref.astype(np.int64))
+
+
+@pytest.mark.parametrize("argmax", [True, False])
+def test_dl64_strided_batched(argmax):
+    """Two batch items, each with its own operand classes (a NaN in item 1
+    only) and, with argmax, its own B^T."""
+    from tropical_gemm import _native as nat, ops
+
+    batch, m, n, k = 2, 512, 4096, 640
+    plan = nat.gemm_plan("maxplus", "f64", m, n, k, argmax, batch=batch,
+                         strides=(m * k, k * n, m * n))
+    assert plan == ("dl64_4x8_cl16" if argmax else "dl64_4x8")
+    rng = np.random.default_rng(92)
+    a = np.round(rng.standard_normal((batch, m, k)) * 4) / 4
+    b = np.round(rng.standard_normal((batch, k, n)) * 4) / 4
+    a[a == 0] = 0.125
+    b[b == 0] = -0.125
+    a[1, 3, k // 2] = np.nan
+    print(f"[case] dl64 batched argmax={argmax}", flush=True)
+    c, am = ops.gemm_batched("maxplus", torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV),
+                             argmax)
+    torch.cuda.synchronize()
+    c = c.cpu().numpy()
+    am = am.cpu().numpy() if argmax else None
+    rows = np.array([0, 3, 64, m - 1])
+    for z in range(batch):
+        c_ref, am_ref = oracle.gemm("maxplus", a[z][rows], b[z])
+        _check_values(c[z][rows], c_ref)
+        if argmax:
+            np.testing.assert_array_equal(am[z][rows].astype(np.int64), am_ref.astype(np.int64))

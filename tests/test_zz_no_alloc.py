@@ -63,6 +63,7 @@ CASES = [
     ("maxplus", "f32", "row", False, (256, 256, 1024), (128, 128, 512), "dl_4x4_cl32 split 4"),
     ("maxmul", "f64", "row", True, (64, 130, 640), (40, 64, 320), "tiles_chunked"),
     ("maxplus", "f64", "row", True, (1024, 4096, 640), (1024, 2048, 576), "dl64_4x8_cl16"),
+    ("minplus", "f64", "row", False, (1024, 4096, 640), (1024, 2048, 576), "dl64_4x8"),
     ("maxplus", "i32", "col", True, (384, 256, 1024), (256, 128, 512), None),
     ("maxplus", "f32", "row", True, (3072, 4096, 1024), (512, 256, 512), "dl_4x8_cl16"),
 ]
