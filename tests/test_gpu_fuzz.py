@@ -6,7 +6,9 @@ K-resident kernel with its three integer paths, split K) over all dtypes, semiri
 and strided-batched, with a caller workspace or the library's own.  Every
 output, the gaps between strided outputs and the workspace are surrounded by
 guard bytes that must come back untouched, and every result must equal the
-oracle bit for bit (values as bit patterns, argmax exactly).
+oracle bit for bit (values as bit patterns, argmax exactly).  The backward
+fuzz does the same for the gradients, which the kernels sum in the
+reference's order.
 """
 import ctypes
 
@@ -182,13 +184,6 @@ def test_forward_fuzz(seed):
                 np.testing.assert_array_equal(it.astype(np.int64), am_ref.astype(np.int64))
 
 
-def _tolerance_ok(got, ref, cnt, abs_sum, eps):
-    """|got - ref| <= 4 * n_terms * eps * sum|terms| per element; exact where a
-    single term lands (the tolerance the backward tests state)."""
-    diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
-    return bool(np.all(diff[cnt <= 1] == 0)) and bool(np.all(diff <= 4 * cnt * eps * abs_sum))
-
-
 @pytest.mark.parametrize("seed", range(4))
 def test_backward_fuzz(seed):
     from tropical_gemm import _native as nat
@@ -200,7 +195,7 @@ def test_backward_fuzz(seed):
         dt = str(rng.choice(["f32", "f64"]))
         m, k, n = (int(x) for x in rng.integers(1, 200, size=3))
         if rng.random() < 0.3:
-            k = int(rng.choice([4096, 9000]))  # LDS-limited and global-atomic fallbacks
+            k = int(rng.choice([4096, 9000]))  # LDS-limited grad_B, and bins in global memory
         layout = str(rng.choice(["row", "col"]))
         mult = bool(rng.random() < 0.4)
         batch = int(rng.choice([1, 2]))
@@ -234,25 +229,14 @@ def test_backward_fuzz(seed):
         torch.cuda.synchronize()
         assert _guards_ok(obuf, batch * o_elems * es), "gradient guard overwritten"
         got = obuf[GUARD:GUARD + batch * o_elems * es].cpu().numpy().view(NP[dt])
-        eps = 2.0**-24 if dt == "f32" else 2.0**-53
         for t in range(batch):
             ot = got[t * o_elems:(t + 1) * o_elems]
             ot = ot.reshape(out_shape[::-1]).T if layout == "col" else ot.reshape(out_shape)
-            amt = am[t].astype(np.int64)
             o = other[t] if mult else None
             if which == "a":
                 ref = oracle.backward_a(g[t], am[t].astype(np.uint32), k, o)
             else:
                 ref = oracle.backward_b(g[t], am[t].astype(np.uint32), k, o)
-            ii, jj = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
-            ok = amt < k
-            terms = np.abs(g[t].astype(np.float64))
-            if mult:
-                kk = np.where(ok, amt, 0)
-                terms = terms * np.abs(o[kk, jj] if which == "a" else o[ii, kk])
-            cnt = np.zeros(out_shape)
-            sab = np.zeros(out_shape)
-            idx = (ii[ok], amt[ok]) if which == "a" else (amt[ok], jj[ok])
-            np.add.at(cnt, idx, 1)
-            np.add.at(sab, idx, terms[ok])
-            assert _tolerance_ok(ot, ref, cnt, sab, eps)
+            # The kernels add in the reference's order: the same bits.
+            np.testing.assert_array_equal(tc.bits(np.ascontiguousarray(ot)),
+                                          tc.bits(np.ascontiguousarray(ref)))
