@@ -25,11 +25,27 @@ def test_more_than_one_gpu_is_refused():
     assert "one GPU" in r.stderr and r.stdout == ""
 
 
+def test_every_config_is_described():
+    """Each --config choice has a workload name, a kernel name and (except
+    the einsum caller) a workloads.py configuration, and either a CPU sample
+    size or a stated reason for having no CPU baseline."""
+    sys.path.insert(0, ROOT)
+    import bench
+    import workloads
+
+    for name in ("P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "F2"):
+        assert name in bench.WORKLOAD_NAMES and name in bench.KERNEL_NAMES, name
+        assert name in workloads.CONFIGS, name
+        assert name == "P" or name in bench.CPU_ROWS or name in bench.NO_CPU_BASELINE, name
+        if workloads.CONFIGS[name]["dtype"] == "f64":
+            assert bench.WORKLOAD_NAMES[name].startswith(f"{name}: MaxPlus f64")
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("args", [("--config", "P", "--cpu-rows", "64"),
                                   ("--config", "C1"),
-                                  ("--config", "M1"), ("--config", "E1")],
-                         ids=["P", "C1", "M1", "E1"])
+                                  ("--config", "M1"), ("--config", "E1"), ("--config", "F2")],
+                         ids=["P", "C1", "M1", "E1", "F2"])
 def test_json_line(args):
     print(f"[case] bench.py {' '.join(args)}", flush=True)
     r = _bench(*args, "--steps", "2", "--warmup", "1")
@@ -54,6 +70,9 @@ def test_json_line(args):
         assert base["value"] > 0 and base["cores"] == 1 and base["kind"] in ("port", "reference")
         assert "argmax" in base["sample"]
         assert out["argmax_consistency_check"] is True
+    if args[1] == "F2":  # f64: against the FP64 vector peak; no CPU restatement, said so
+        assert roof["unit"] == "TFLOP/s" and roof["peak"] == 78.6 and out["dtype"] == "f64"
+        assert "cpu_baseline" not in out and out["cpu_baseline_note"]
     if args[1] == "C1":  # the reference's value-only CPU path on the same product
         base = out["cpu_baseline_value_only"]
         assert base["value"] > 0 and base["cores"] == 1 and "AVX2" in base["sample"]
