@@ -169,6 +169,25 @@ bool aligned16(const void* p) {
     return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// B^T staging (BT[z][j][k] = B[z][k][j], nb batch items): 16-byte vectors when
+// the shape, strides and pointers allow them, element by element otherwise.
+// The callers have checked (K + 31) / 32 <= 65535.
+template <typename T>
+int launch_transpose(const T* B, T* BT, int64_t K, int64_t N, int64_t sB, int64_t sBT, int64_t nb,
+                     hipStream_t st) {
+    constexpr int VW = tg::Vec16<T>::N;
+    if (K % VW == 0 && N % VW == 0 && sB % VW == 0 && sBT % VW == 0 && aligned16<T>(B) &&
+        aligned16<T>(BT)) {
+        dim3 grid(unsigned((N + 63) / 64), unsigned((K + 63) / 64), unsigned(nb));
+        hipLaunchKernelGGL((tg::tg_transpose_v<T>), grid, dim3(256), 0, st, B, BT, K, N, sB, sBT);
+    } else {
+        dim3 grid(unsigned((N + 31) / 32), unsigned((K + 31) / 32), unsigned(nb));
+        hipLaunchKernelGGL((tg::tg_transpose<T>), grid, dim3(32, 8), 0, st, B, BT, K, N, sB, sBT);
+    }
+    TG_HIP(hipGetLastError());
+    return TG_OK;
+}
+
 // Row-major problem description after the layout mapping.
 struct Problem {
     const void* A;
@@ -245,10 +264,9 @@ int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
                            clsB + z0 * p.N);
         TG_HIP(hipGetLastError());
         if (argmax) {
-            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
-            hipLaunchKernelGGL((tg::tg_transpose<double>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB,
-                               BT + z0 * p.K * p.N, p.K, p.N, p.sB, p.K * p.N);
-            TG_HIP(hipGetLastError());
+            const int rc = launch_transpose<double>(B + z0 * p.sB, BT + z0 * p.K * p.N, p.K, p.N,
+                                                    p.sB, p.K * p.N, nb, st);
+            if (rc != TG_OK) return rc;
         }
     }
     KernelTimer timer(st);
@@ -299,10 +317,8 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
             const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
             T* BT = reinterpret_cast<T*>(wsb + wl.bt) + z0 * p.K * p.N;
-            dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
-            hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, B + z0 * p.sB, BT,
-                               p.K, p.N, p.sB, p.K * p.N);
-            TG_HIP(hipGetLastError());
+            const int rc = launch_transpose<T>(B + z0 * p.sB, BT, p.K, p.N, p.sB, p.K * p.N, nb, st);
+            if (rc != TG_OK) return rc;
         }
     }
     // 128 x 128 value-only tiles take 64 KB of dynamic LDS: raise the
@@ -753,10 +769,8 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
             if (p.K > 0) {
                 if ((p.K + 31) / 32 > 65535)
                     return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
-                dim3 tgrid(unsigned((p.N + 31) / 32), unsigned((p.K + 31) / 32), unsigned(nb));
-                hipLaunchKernelGGL((tg::tg_transpose<T>), tgrid, dim3(32, 8), 0, st, Bz, BT, p.K,
-                                   p.N, p.sB, sBT);
-                TG_HIP(hipGetLastError());
+                const int rc = launch_transpose<T>(Bz, BT, p.K, p.N, p.sB, sBT, nb, st);
+                if (rc != TG_OK) return rc;
             }
             KernelTimer timer(st);
             if (vec)

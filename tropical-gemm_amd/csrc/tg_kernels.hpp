@@ -587,6 +587,51 @@ __global__ __launch_bounds__(256) void tg_transpose(const T* __restrict__ B, T* 
 }
 
 // ---------------------------------------------------------------------------
+// The same with 16-byte vectors (VW = 16 / sizeof(T) elements) on 64 x 64
+// tiles: every load reads VW columns of a row of B, every store writes VW
+// k of a row of B^T.  Requires K and N multiples of VW, 16-byte aligned B and
+// BT, and batch strides multiples of VW (then a vector is either wholly in
+// the matrix or wholly out).  The LDS rows are padded to 65 elements, which
+// spreads the column reads of a wave over the banks.
+// grid = (ceil(N/64), ceil(K/64), batch), block = 256.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void tg_transpose_v(const T* __restrict__ B, T* __restrict__ BT,
+                                                      int64_t K, int64_t N, int64_t sB, int64_t sBT) {
+    constexpr int VW = Vec16<T>::N;
+    constexpr int TS = 64, LD = TS + 1;
+    constexpr int VPR = TS / VW;    // vectors per tile row
+    constexpr int RPP = 256 / VPR;  // tile rows per pass
+    __shared__ T tile[TS * LD];
+    const int64_t z = blockIdx.z;
+    B += z * sB;
+    BT += z * sBT;
+    const int64_t n0 = int64_t(blockIdx.x) * TS;
+    const int64_t k0 = int64_t(blockIdx.y) * TS;
+    const int v = threadIdx.x % VPR, r = threadIdx.x / VPR;
+#pragma unroll
+    for (int rr = r; rr < TS; rr += RPP) {  // rr: k in the tile, v: a vector of n
+        const int64_t k = k0 + rr, n = n0 + v * VW;
+        if (k < K && n < N) {
+            const Vec16<T> x = *reinterpret_cast<const Vec16<T>*>(B + k * N + n);
+#pragma unroll
+            for (int e = 0; e < VW; ++e) tile[rr * LD + v * VW + e] = x.v[e];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rr = r; rr < TS; rr += RPP) {  // rr: n in the tile, v: a vector of k
+        const int64_t n = n0 + rr, k = k0 + v * VW;
+        if (n < N && k < K) {
+            Vec16<T> y;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) y.v[e] = tile[(v * VW + e) * LD + rr];
+            *reinterpret_cast<Vec16<T>*>(BT + n * K + k) = y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Zero fill (16-byte stores + byte tail).  Used instead of hipMemsetAsync so
 // that the library records no memset nodes when a caller captures a graph.
 // ---------------------------------------------------------------------------
