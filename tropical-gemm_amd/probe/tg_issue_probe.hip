@@ -10,6 +10,10 @@
 //   f32, A in SGPRs:  the same with one operand wave-uniform (scalar loads)
 //   f64:              v_add_f64 x2 + v_max_f64 x2 per 2 products (no
 //                     three-input f64 max on gfx950)
+//   f32, DPP operand: the VGPR mix with the second add's B operand read
+//                     from the partner lane (lane ^ 1) through DPP, the
+//                     operand feed that would let lane pairs share B
+//                     fragments instead of each reading them from LDS
 // Grid: 256 workgroups x waves_per_simd of 256 threads (4 waves, one per
 // SIMD), so waves/SIMD = 1, 2, 4 or 8 across the sweep.
 //
@@ -33,7 +37,19 @@
         }                                                                            \
     } while (0)
 
-enum Mix { F32_VGPR = 0, F32_SGPR = 1, F32_IEEE = 2, F64_VGPR = 3 };
+enum Mix { F32_VGPR = 0, F32_SGPR = 1, F32_IEEE = 2, F64_VGPR = 3, F32_DPP = 4 };
+
+// d = bsrc(lane ^ 1) + a: v_add_f32 with a DPP quad permutation on its first
+// operand.  bsrc must not be written by a VALU instruction in the two
+// instructions before (the DPP read hazard): the probe never writes it in
+// the loop.
+__device__ __forceinline__ float add_partner(float bsrc, float a) {
+    float d;
+    asm volatile("v_add_f32_dpp %0, %1, %2 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf"
+                 : "=v"(d)
+                 : "v"(bsrc), "v"(a));
+    return d;
+}
 
 template <typename T, int MIX>
 __global__ __launch_bounds__(256) void chains(const T* __restrict__ a_in, const T* __restrict__ b_in,
@@ -57,12 +73,16 @@ __global__ __launch_bounds__(256) void chains(const T* __restrict__ a_in, const 
     T acc[8][4];
     for (int r = 0; r < 8; ++r)
         for (int j = 0; j < 4; ++j) acc[r][j] = T(-1e30);
+    if constexpr (MIX == F32_DPP) asm volatile("s_nop 4" ::: "memory");  // b2 settled for DPP
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if constexpr (MIX == F32_IEEE)
+                if constexpr (MIX == F32_DPP)
+                    acc[r][j] = __builtin_fmax(__builtin_fmax(acc[r][j], a[r] + b[j]),
+                                               add_partner(b2[j], a2[r]));
+                else if constexpr (MIX == F32_IEEE)
                     acc[r][j] = __builtin_elementwise_maximum(
                         __builtin_elementwise_maximum(acc[r][j], a[r] + b[j]), a2[r] + b2[j]);
                 else
@@ -71,7 +91,7 @@ __global__ __launch_bounds__(256) void chains(const T* __restrict__ a_in, const 
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             b[j] = b[j] + T(0.5);
-            b2[j] = b2[j] - T(0.25);
+            if constexpr (MIX != F32_DPP) b2[j] = b2[j] - T(0.25);  // DPP: b2 stays put
         }
     }
     T s = 0;
@@ -175,6 +195,7 @@ int main() {
         run<float, F32_IEEE>("f32 add+maximum3, A in VGPR", wps, iters, 64 + 32 + 8);
         run<float, F32_SGPR>("f32 add+max3, A in SGPR", wps, iters, 64 + 32 + 8);
         run<double, F64_VGPR>("f64 add+max, A in VGPR", wps, iters, 64 + 64 + 8);
+        run<float, F32_DPP>("f32 add+max3, B2 via DPP", wps, iters, 64 + 32 + 4);
     }
     for (int w = 1; w <= 4; ++w) {
         run_lds<64>("LDS b128, 64 distinct/wave", w, 4000);
