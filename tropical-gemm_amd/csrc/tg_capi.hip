@@ -173,14 +173,24 @@ bool aligned16(const void* p) {
 // the shape, strides and pointers allow them, element by element otherwise.
 // The callers have checked (K + 31) / 32 <= 65535.
 template <typename T>
-int launch_transpose(const T* B, T* BT, int64_t K, int64_t N, int64_t sB, int64_t sBT, int64_t nb,
-                     hipStream_t st) {
+bool transpose_vectors(const T* B, const T* BT, int64_t K, int64_t N, int64_t sB, int64_t sBT) {
     constexpr int VW = tg::Vec16<T>::N;
-    if (K % VW == 0 && N % VW == 0 && sB % VW == 0 && sBT % VW == 0 && aligned16<T>(B) &&
-        aligned16<T>(BT)) {
+    return K % VW == 0 && N % VW == 0 && sB % VW == 0 && sBT % VW == 0 && aligned16<T>(B) &&
+           aligned16<T>(BT);
+}
+
+// cls (f64 only, and only where transpose_vectors holds): the column classes
+// of B are ORed into cls[z*N + j] on the way (see tg_transpose_v).
+template <typename T>
+int launch_transpose(const T* B, T* BT, int64_t K, int64_t N, int64_t sB, int64_t sBT, int64_t nb,
+                     hipStream_t st, uint32_t* cls = nullptr) {
+    if (transpose_vectors<T>(B, BT, K, N, sB, sBT)) {
         dim3 grid(unsigned((N + 63) / 64), unsigned((K + 63) / 64), unsigned(nb));
-        hipLaunchKernelGGL((tg::tg_transpose_v<T>), grid, dim3(256), 0, st, B, BT, K, N, sB, sBT);
+        hipLaunchKernelGGL((tg::tg_transpose_v<T>), grid, dim3(256), 0, st, B, BT, K, N, sB, sBT,
+                           cls);
     } else {
+        if (cls != nullptr)
+            return fail(TG_ERR_INVALID_ARGUMENT, "internal: column classes need the vector transpose");
         dim3 grid(unsigned((N + 31) / 32), unsigned((K + 31) / 32), unsigned(nb));
         hipLaunchKernelGGL((tg::tg_transpose<T>), grid, dim3(32, 8), 0, st, B, BT, K, N, sB, sBT);
     }
@@ -247,27 +257,29 @@ int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
     uint32_t* cls = reinterpret_cast<uint32_t*>(wsb + bt_bytes);
     uint32_t* clsA = cls;
     uint32_t* clsB = cls + p.batch * p.M;
+    // With argmax, the B^T transpose records the column classes when it runs
+    // on 16-byte vectors (every batch chunk alike: sB and K*N are even).
+    const bool cols_in_transpose =
+        argmax && transpose_vectors<double>(B, BT, p.K, p.N, p.sB, p.K * p.N);
     hipLaunchKernelGGL(tg::tg_fill_zero, dim3(unsigned((p.batch * (p.M + p.N) * 4 / 16 + 255) / 256 + 1)),
                        dim3(256), 0, st, reinterpret_cast<unsigned char*>(cls), p.batch * (p.M + p.N) * 4);
     TG_HIP(hipGetLastError());
     {
-        int64_t blocks = (p.batch * p.M + 3) / 4;
-        if (blocks > 16384) blocks = 16384;
-        hipLaunchKernelGGL(tg::tg_class_rows, dim3(unsigned(blocks)), dim3(256), 0, st, A, p.M, p.K,
-                           p.sA, p.batch, clsA);
+        int64_t row_blocks = (p.batch * p.M + 3) / 4;
+        if (row_blocks > 16384) row_blocks = 16384;
+        int64_t col_blocks = cols_in_transpose ? 0 : ((p.N + 63) / 64) * ((p.K + 255) / 256) * p.batch;
+        if (col_blocks > 16384) col_blocks = 16384;
+        hipLaunchKernelGGL(tg::tg_class_prepass, dim3(unsigned(row_blocks + col_blocks)), dim3(256), 0,
+                           st, A, p.M, p.K, p.sA, B, p.N, p.sB, p.batch, clsA,
+                           cols_in_transpose ? nullptr : clsB, int(row_blocks));
         TG_HIP(hipGetLastError());
     }
-    for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+    for (int64_t z0 = 0; argmax && z0 < p.batch; z0 += 65535) {
         const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
-        dim3 cgrid(unsigned((p.N + 63) / 64), unsigned((p.K + 255) / 256), unsigned(nb));
-        hipLaunchKernelGGL(tg::tg_class_cols, cgrid, dim3(256), 0, st, B + z0 * p.sB, p.K, p.N, p.sB,
-                           clsB + z0 * p.N);
-        TG_HIP(hipGetLastError());
-        if (argmax) {
-            const int rc = launch_transpose<double>(B + z0 * p.sB, BT + z0 * p.K * p.N, p.K, p.N,
-                                                    p.sB, p.K * p.N, nb, st);
-            if (rc != TG_OK) return rc;
-        }
+        const int rc = launch_transpose<double>(B + z0 * p.sB, BT + z0 * p.K * p.N, p.K, p.N, p.sB,
+                                                p.K * p.N, nb, st,
+                                                cols_in_transpose ? clsB + z0 * p.N : nullptr);
+        if (rc != TG_OK) return rc;
     }
     KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {

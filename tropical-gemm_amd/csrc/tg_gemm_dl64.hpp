@@ -57,18 +57,6 @@ struct Dl64Cfg {
     static constexpr int LDS_BYTES = (MISC_OFF + 64 > TILE_BYTES) ? MISC_OFF + 64 : TILE_BYTES;
 };
 
-// Operand classes for the NaN check: bits of a row of A or a column of B.
-enum : uint32_t { TG_CLS_NAN = 1, TG_CLS_PINF = 2, TG_CLS_NINF = 4, TG_CLS_ZERO = 8 };
-
-__device__ __forceinline__ uint32_t tclass(double x) {
-    uint32_t c = 0;
-    if (x != x) c |= TG_CLS_NAN;
-    if (x == __builtin_huge_val()) c |= TG_CLS_PINF;
-    if (x == -__builtin_huge_val()) c |= TG_CLS_NINF;
-    if (x == 0.0) c |= TG_CLS_ZERO;
-    return c;
-}
-
 // True when a row of class ca and a column of class cb can make a NaN
 // product at some k (conservative: the k need not coincide).
 template <int SR>
@@ -82,40 +70,52 @@ __device__ __forceinline__ bool nan_danger(uint32_t ca, uint32_t cb) {
     }
 }
 
-// Classes of the rows of A (batch x M x K, batch stride sA) into cls[z*M + i]
-// (zeroed beforehand).  One wave per row at a time, grid-stride.
-__global__ __launch_bounds__(256) void tg_class_rows(const double* __restrict__ A, int64_t M,
-                                                     int64_t K, int64_t sA, int64_t batch,
-                                                     uint32_t* __restrict__ cls) {
+// Operand classes, one launch: blocks [0, row_blocks) take the rows of A
+// (batch x M x K, batch stride sA) into clsA[z*M + i], one wave per row at a
+// time; the other blocks take the columns of B (batch x K x N, batch stride
+// sB) into clsB[z*N + j] (skipped when clsB is null: the f64 argmax path
+// gets them from the B^T transpose, which reads B anyway), in segments of 64
+// columns x 256 k, 4 k-lanes per column.  Both arrays zeroed beforehand.
+// Grid-stride over rows and segments; block = 256.
+__global__ __launch_bounds__(256) void tg_class_prepass(const double* __restrict__ A, int64_t M,
+                                                        int64_t K, int64_t sA,
+                                                        const double* __restrict__ B, int64_t N,
+                                                        int64_t sB, int64_t batch,
+                                                        uint32_t* __restrict__ clsA,
+                                                        uint32_t* __restrict__ clsB,
+                                                        int row_blocks) {
     const int lane = threadIdx.x & 63;
-    const int64_t waves = int64_t(gridDim.x) * 4;
-    for (int64_t w = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); w < batch * M; w += waves) {
-        const int64_t z = w / M, i = w - z * M;
-        const double* row = A + z * sA + i * K;
-        uint32_t c = 0;
-        for (int64_t k = lane; k < K; k += 64) c |= tclass(row[k]);
-        uint32_t all = 0;
+    if (int(blockIdx.x) < row_blocks) {
+        const int64_t waves = int64_t(row_blocks) * 4;
+        for (int64_t w = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6); w < batch * M; w += waves) {
+            const int64_t z = w / M, i = w - z * M;
+            const double* row = A + z * sA + i * K;
+            uint32_t c = 0;
+            for (int64_t k = lane; k < K; k += 64) c |= tclass(row[k]);
+            uint32_t all = 0;
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-            if (__ballot((c >> b) & 1u)) all |= 1u << b;
-        if (lane == 0) cls[w] = all;
+            for (int b = 0; b < 4; ++b)
+                if (__ballot((c >> b) & 1u)) all |= 1u << b;
+            if (lane == 0) clsA[w] = all;
+        }
+        return;
     }
-}
-
-// Classes of the columns of B (batch x K x N, batch stride sB) into
-// cls[z*N + j] (zeroed beforehand).  grid = (ceil(N / 64), ceil(K / 256),
-// batch), block = 256: 64 columns x 4 k-lanes, each k-lane walking 64 k.
-__global__ __launch_bounds__(256) void tg_class_cols(const double* __restrict__ B, int64_t K,
-                                                     int64_t N, int64_t sB,
-                                                     uint32_t* __restrict__ cls) {
-    const int64_t z = blockIdx.z;
-    const int64_t j = int64_t(blockIdx.x) * 64 + (threadIdx.x & 63);
-    const int64_t k0 = int64_t(blockIdx.y) * 256 + (threadIdx.x >> 6);
-    if (j >= N) return;
-    const double* col = B + z * sB + j;
-    uint32_t c = 0;
-    for (int64_t k = k0; k < K && k < k0 + 256; k += 4) c |= tclass(col[k * N]);
-    if (c) atomicOr(cls + z * N + j, c);
+    if (clsB == nullptr) return;
+    const int64_t nbx = (N + 63) / 64, nby = (K + 255) / 256;
+    const int64_t per_z = nbx * nby, segs = per_z * batch;
+    const int64_t cblocks = int64_t(gridDim.x) - row_blocks;
+    for (int64_t sg = int64_t(blockIdx.x) - row_blocks; sg < segs; sg += cblocks) {
+        const int64_t z = sg / per_z, r = sg - z * per_z;
+        const int64_t by = r / nbx, bx = r - by * nbx;
+        const int64_t j = bx * 64 + lane;
+        const int64_t k0 = by * 256 + (threadIdx.x >> 6);
+        if (j < N) {
+            const double* col = B + z * sB + j;
+            uint32_t c = 0;
+            for (int64_t k = k0; k < K && k < k0 + 256; k += 4) c |= tclass(col[k * N]);
+            if (c) atomicOr(clsB + z * N + j, c);
+        }
+    }
 }
 
 // Chunk records of four f64 outputs (record4 with 64-bit compares): ch[q] = c

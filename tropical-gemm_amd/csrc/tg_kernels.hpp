@@ -586,18 +586,35 @@ __global__ __launch_bounds__(256) void tg_transpose(const T* __restrict__ B, T* 
     }
 }
 
+// Operand classes for the NaN check of the f64 kernel: bits of a row of A or
+// a column of B.
+enum : uint32_t { TG_CLS_NAN = 1, TG_CLS_PINF = 2, TG_CLS_NINF = 4, TG_CLS_ZERO = 8 };
+
+__device__ __forceinline__ uint32_t tclass(double x) {
+    uint32_t c = 0;
+    if (x != x) c |= TG_CLS_NAN;
+    if (x == __builtin_huge_val()) c |= TG_CLS_PINF;
+    if (x == -__builtin_huge_val()) c |= TG_CLS_NINF;
+    if (x == 0.0) c |= TG_CLS_ZERO;
+    return c;
+}
+
 // ---------------------------------------------------------------------------
 // The same with 16-byte vectors (VW = 16 / sizeof(T) elements) on 64 x 64
 // tiles: every load reads VW columns of a row of B, every store writes VW
 // k of a row of B^T.  Requires K and N multiples of VW, 16-byte aligned B and
 // BT, and batch strides multiples of VW (then a vector is either wholly in
 // the matrix or wholly out).  The LDS rows are padded to 65 elements, which
-// spreads the column reads of a wave over the banks.
+// spreads the column reads of a wave over the banks.  With T = double and
+// cls non-null, the loads also OR the class bits of each column of B into
+// cls[z*N + j] (zeroed beforehand; atomics only for columns with a bit set),
+// so the f64 kernel needs no separate column pass.
 // grid = (ceil(N/64), ceil(K/64), batch), block = 256.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void tg_transpose_v(const T* __restrict__ B, T* __restrict__ BT,
-                                                      int64_t K, int64_t N, int64_t sB, int64_t sBT) {
+                                                      int64_t K, int64_t N, int64_t sB, int64_t sBT,
+                                                      uint32_t* __restrict__ cls) {
     constexpr int VW = Vec16<T>::N;
     constexpr int TS = 64, LD = TS + 1;
     constexpr int VPR = TS / VW;    // vectors per tile row
@@ -609,13 +626,24 @@ __global__ __launch_bounds__(256) void tg_transpose_v(const T* __restrict__ B, T
     const int64_t n0 = int64_t(blockIdx.x) * TS;
     const int64_t k0 = int64_t(blockIdx.y) * TS;
     const int v = threadIdx.x % VPR, r = threadIdx.x / VPR;
+    uint32_t cl[VW] = {};
 #pragma unroll
     for (int rr = r; rr < TS; rr += RPP) {  // rr: k in the tile, v: a vector of n
         const int64_t k = k0 + rr, n = n0 + v * VW;
         if (k < K && n < N) {
             const Vec16<T> x = *reinterpret_cast<const Vec16<T>*>(B + k * N + n);
 #pragma unroll
-            for (int e = 0; e < VW; ++e) tile[rr * LD + v * VW + e] = x.v[e];
+            for (int e = 0; e < VW; ++e) {
+                tile[rr * LD + v * VW + e] = x.v[e];
+                if constexpr (std::is_same<T, double>::value) cl[e] |= tclass(x.v[e]);
+            }
+        }
+    }
+    if constexpr (std::is_same<T, double>::value) {
+        if (cls != nullptr) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e)
+                if (cl[e]) atomicOr(cls + z * N + n0 + v * VW + e, cl[e]);
         }
     }
     __syncthreads();
