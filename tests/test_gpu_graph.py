@@ -5,7 +5,8 @@ allocation, no memset: buffers that must start at zero are cleared by a fill
 kernel), so a caller can capture it in a HIP graph and replay it.  The test
 captures the forward paths (direct-to-LDS tiles with B^T staging, 64x128
 tiles, split K, the K-resident kernel, the generic tiles, their exact
-short-K mode, value-only) and both backward scatters, replays the graph
+short-K mode, value-only, and the f64 direct-to-LDS kernel with its operand
+class prepass, with and without argmax) and both backward scatters, replays the graph
 several times with new inputs copied in and eager work between the replays,
 and checks every replay against eager calls on the same inputs, bit for bit
 (the backward too: each gradient element receives a single contribution, so
@@ -29,6 +30,8 @@ CASES = [
     ("generic tiles", "minplus", torch.float64, 77, 45, 93, True),
     ("exact short K", "maxplus", torch.float32, 1000, 16, 1024, True),
     ("value-only", "maxmul", torch.float32, 256, 256, 192, False),
+    ("f64 direct-to-LDS", "maxplus", torch.float64, 1024, 640, 4096, True),
+    ("f64 value-only", "minplus", torch.float64, 1024, 256, 4096, False),
 ]
 
 
