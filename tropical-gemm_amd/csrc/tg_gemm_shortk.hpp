@@ -148,16 +148,28 @@ __global__ __launch_bounds__(256) void tg_gemm_shortk(
                     cpu_select<SR, T>(A + (r0 + r) * K, 1, B + col + j, N, K, acc[r][j], unused);
                 }
     }
+    // Non-temporal stores where one instruction writes a contiguous 1 KB run
+    // (32-bit C, and the argmax): 2-3% faster with argmax and 15% value-only
+    // (65536 x 2048 x 16) than plain stores.  64-bit C stays plain: there a
+    // 16-byte store covers every other 16 bytes of the run, and non-temporal
+    // stores of such halves took f64 argmax (32768 x 2048 x 8) 137 -> 234 us.
+    typedef uint32_t U4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (r0 + r >= M) break;
         const int64_t off = (r0 + r) * N + col;
+        if constexpr (VN == 4) {
+            __builtin_nontemporal_store(*reinterpret_cast<const U4*>(acc[r]),
+                                        reinterpret_cast<U4*>(C + off));
+        } else {
 #pragma unroll
-        for (int h = 0; h < 4 / VN; ++h)
-            reinterpret_cast<Vec16<T>*>(C + off)[h] = reinterpret_cast<const Vec16<T>*>(acc[r])[h];
+            for (int h = 0; h < 4 / VN; ++h)
+                reinterpret_cast<Vec16<T>*>(C + off)[h] =
+                    reinterpret_cast<const Vec16<T>*>(acc[r])[h];
+        }
         if constexpr (ARGMAX)
-            *reinterpret_cast<Vec16<int32_t>*>(IDX + off) =
-                *reinterpret_cast<const Vec16<int32_t>*>(ix[r]);
+            __builtin_nontemporal_store(*reinterpret_cast<const U4*>(ix[r]),
+                                        reinterpret_cast<U4*>(IDX + off));
     }
 }
 
