@@ -23,8 +23,9 @@
 // windows.
 //
 // NaN: v_max_f64 / v_min_f64 return the other operand of a NaN, so a chain
-// never shows a NaN product.  A prepass (tg_class_rows / tg_class_cols)
-// records per row of A and per column of B whether it holds a NaN, +inf,
+// never shows a NaN product.  A prepass (tg_class_prepass; with argmax the
+// B^T transpose does the columns) records per row of A and per column of B
+// whether it holds a NaN, +inf,
 // -inf or a zero; an output whose row and column could meet in a NaN product
 // (a NaN operand, +inf with -inf for MaxPlus / MinPlus, a zero with an
 // infinity for MaxMul) is recomputed after the stores with the reference's
