@@ -95,10 +95,11 @@ def cpu_model() -> str:
 # Rows of each configuration's CPU-baseline sample outside P (P: --cpu-rows):
 # about 0.5-4 s of single-core work.  C1 and C4 run whole; M1's short K makes
 # the reference's blocked loops slow (0.07 GOP/s), hence its small slab.
-CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096, "F1": 256}
+CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096, "F1": 256,
+            "F2": 4096}
 # Configurations without a CPU restatement of the reference path they would
-# take (the reference's f64 value-only SIMD kernels are not restated).
-NO_CPU_BASELINE = {"F2": "no restatement of the reference's f64 value-only SIMD path"}
+# take, with the reason (none at present: every configuration has one).
+NO_CPU_BASELINE: dict = {}
 
 
 def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> dict:
@@ -106,7 +107,9 @@ def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> di
     configuration, timed on the first ``rows`` rows of the same inputs:
     argmax configurations run the reference's argmax path (BLIS PORTABLE
     tiling, 4x4 scalar microkernel); value-only f32 ones (and C1's
-    value-only line) its AVX2 path (F32_AVX2 tiling, 8x8 microkernel)."""
+    value-only line) its AVX2 path (F32_AVX2 tiling, 8x8 microkernel);
+    value-only MaxPlus f64 its AVX2 f64 path (F64_AVX2 tiling, 4x4
+    microkernel)."""
     import numpy as np
 
     from oracle import oracle
@@ -123,6 +126,9 @@ def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> di
     elif ha.dtype == np.float32:
         fn, algo = oracle.avx2_gemm_f32, ("value-only algorithm (BLIS F32_AVX2 tiling, AVX2 8x8 "
                                           "microkernel)")
+    elif ha.dtype == np.float64 and sr == "maxplus":
+        fn, algo = oracle.avx2_gemm_maxplus_f64, ("value-only algorithm (BLIS F64_AVX2 tiling, AVX2 "
+                                                  "4x4 f64 microkernel)")
     else:
         raise ValueError("no CPU baseline restated for this configuration")
     t0 = time.perf_counter()

@@ -63,6 +63,8 @@ def _load():
             fn.restype = ctypes.c_int
         lib.tgo_avx2_gemm_f32.argtypes = [ctypes.c_int, vp, vp, vp, i64, i64, i64]
         lib.tgo_avx2_gemm_f32.restype = ctypes.c_int
+        lib.tgo_avx2_gemm_maxplus_f64.argtypes = [vp, vp, vp, i64, i64, i64]
+        lib.tgo_avx2_gemm_maxplus_f64.restype = ctypes.c_int
         _lib = lib
     return _lib
 
@@ -161,6 +163,25 @@ def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
 def portable_argmax_f32(semiring: str, a: np.ndarray, b: np.ndarray):
     """float32 form of ``portable_argmax``."""
     return portable_argmax(semiring, np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
+
+
+def avx2_gemm_maxplus_f64(semiring: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Single-thread restatement of the reference CPU value-only MaxPlus f64
+    path (BLIS F64_AVX2 tiling + AVX2 4x4 f64 microkernel,
+    simd/kernels/avx2.rs:77-143); used as the timed baseline of value-only
+    f64 MaxPlus configurations.  The reference runs MinPlus and MaxMul f64
+    on its portable path, which has no value-only restatement here."""
+    if semiring != "maxplus":
+        raise ValueError("the reference's AVX2 f64 kernel is MaxPlus only")
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    b = np.ascontiguousarray(b, dtype=np.float64)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), dtype=np.float64)
+    rc = _load().tgo_avx2_gemm_maxplus_f64(_ptr(a), _ptr(b), _ptr(c), m, n, k)
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return c
 
 
 def avx2_gemm_f32(semiring: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -30,8 +30,8 @@
  *     pthreads.  Results are therefore identical to the reference CPU path
  *     for every non-NaN input (NaN handling also follows the select rule).
  *
- *  2. tgo_portable_argmax_{f32,f64,i32} and tgo_avx2_gemm_f32 : the CPU
- *     BASELINES used for timing.  Faithful single-thread restatements of the
+ *  2. tgo_portable_argmax_{f32,f64,i32}, tgo_avx2_gemm_f32 and
+ *     tgo_avx2_gemm_maxplus_f64 : the CPU BASELINES used for timing.  Faithful single-thread restatements of the
  *     reference's two CPU paths:
  *       argmax (every dtype): BLIS 5-loop with TilingParams::PORTABLE
  *       (MC=NC=64, KC=256, MR=NR=4; core/tiling.rs:39-45), pack_a/pack_b
@@ -40,7 +40,12 @@
  *       value-only f32: the same 5-loop with TilingParams::F32_AVX2 (MC=NC=
  *       256, KC=512, MR=NR=8) and the AVX2 8x8 microkernel
  *       (simd/kernels/avx2.rs), which the reference dispatches to on AVX2 and
- *       AVX-512 hosts alike (simd/dispatch.rs).
+ *       AVX-512 hosts alike (simd/dispatch.rs);
+ *       value-only MaxPlus f64: the 5-loop with TilingParams::F64_AVX2 (MC=NC=
+ *       128, KC=256, MR=NR=4; core/tiling.rs:29-35) and the AVX2 4x4 f64
+ *       microkernel (simd/kernels/avx2.rs:77-143; simd/dispatch.rs:86-108).
+ *       MinPlus and MaxMul f64 take the portable path there
+ *       (simd/dispatch.rs:233-243), so they have no restatement here.
  *     Their results equal the oracle's on ordinary data; they exist so the
  *     timed numbers reflect the reference's algorithms, not the oracle's
  *     vectorised loop.
@@ -460,6 +465,97 @@ int tgo_avx2_gemm_f32(int sr, const float* A, const float* B, float* C, int64_t 
                         const int64_t mr = mc - i0 < V_MR ? mc - i0 : V_MR;
                         vmicro_f32(sr, mr, nr, kc, pa + ir * V_MR * kc, pb + jr * V_NR * kc,
                                    C + (ic + i0) * N + (jc + j0), N);
+                    }
+                }
+            }
+        }
+    }
+    free(pa);
+    free(pb);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* CPU BASELINE for value-only MaxPlus f64: the reference's AVX2 path        */
+/* (simd/kernels/avx2.rs:77-143: a 4x4 microkernel on f64x4 rows, per k     */
+/*  acc[i] = max(acc[i], A[i,k] + B[k,0..3]); core/gemm.rs:81-134 driver;    */
+/*  tiling.rs:29-35 F64_AVX2 = MC 128, NC 128, KC 256, MR 4, NR 4).          */
+/* ------------------------------------------------------------------------ */
+#define D_MC 128
+#define D_NC 128
+#define D_KC 256
+#define D_MR 4
+#define D_NR 4
+
+static void dpack_a_f64(int64_t mc, int64_t kc, const double* a, int64_t lda, double* packed) {
+    int64_t p = 0;
+    for (int64_t r0 = 0; r0 < mc; r0 += D_MR)
+        for (int64_t col = 0; col < kc; ++col)
+            for (int64_t ro = 0; ro < D_MR; ++ro) {
+                const int64_t row = r0 + ro;
+                packed[p++] = row < mc ? a[row * lda + col] : 0.0;
+            }
+}
+
+static void dpack_b_f64(int64_t kc, int64_t nc, const double* b, int64_t ldb, double* packed) {
+    int64_t p = 0;
+    for (int64_t c0 = 0; c0 < nc; c0 += D_NR)
+        for (int64_t row = 0; row < kc; ++row)
+            for (int64_t co = 0; co < D_NR; ++co) {
+                const int64_t col = c0 + co;
+                packed[p++] = col < nc ? b[row * ldb + col] : 0.0;
+            }
+}
+
+static void dmicro_maxplus_f64(int64_t mr, int64_t nr, int64_t kc, const double* pa,
+                               const double* pb, double* c, int64_t ldc) {
+    __m256d acc[D_MR];
+    for (int64_t i = 0; i < D_MR; ++i) {
+        double row[D_NR];
+        for (int64_t j = 0; j < D_NR; ++j) row[j] = (i < mr && j < nr) ? c[i * ldc + j] : -INFINITY;
+        acc[i] = _mm256_loadu_pd(row);
+    }
+    for (int64_t p = 0; p < kc; ++p) {
+        const __m256d bv = _mm256_loadu_pd(pb + p * D_NR);
+        for (int64_t i = 0; i < D_MR; ++i)
+            acc[i] = _mm256_max_pd(acc[i], _mm256_add_pd(_mm256_set1_pd(pa[p * D_MR + i]), bv));
+    }
+    for (int64_t i = 0; i < mr; ++i) {
+        double row[D_NR];
+        _mm256_storeu_pd(row, acc[i]);
+        for (int64_t j = 0; j < nr; ++j) c[i * ldc + j] = row[j];
+    }
+}
+
+/* Row-major value-only MaxPlus C = A (x) B; C is initialised to -inf. */
+int tgo_avx2_gemm_maxplus_f64(const double* A, const double* B, double* C, int64_t M, int64_t N,
+                              int64_t K) {
+    if (M < 0 || N < 0 || K < 0) return -1;
+    for (int64_t t = 0; t < M * N; ++t) C[t] = -INFINITY;
+    if (M == 0 || N == 0 || K == 0) return 0;
+    double* pa = (double*)malloc(sizeof(double) * D_MC * D_KC);
+    double* pb = (double*)malloc(sizeof(double) * D_KC * D_NC);
+    if (!pa || !pb) {
+        free(pa);
+        free(pb);
+        return -2;
+    }
+    for (int64_t jc = 0; jc < N; jc += D_NC) {
+        const int64_t nc = N - jc < D_NC ? N - jc : D_NC;
+        for (int64_t pc = 0; pc < K; pc += D_KC) {
+            const int64_t kc = K - pc < D_KC ? K - pc : D_KC;
+            dpack_b_f64(kc, nc, B + pc * N + jc, N, pb);
+            for (int64_t ic = 0; ic < M; ic += D_MC) {
+                const int64_t mc = M - ic < D_MC ? M - ic : D_MC;
+                dpack_a_f64(mc, kc, A + ic * K + pc, K, pa);
+                for (int64_t jr = 0; jr * D_NR < nc; ++jr) {
+                    const int64_t j0 = jr * D_NR;
+                    const int64_t nr = nc - j0 < D_NR ? nc - j0 : D_NR;
+                    for (int64_t ir = 0; ir * D_MR < mc; ++ir) {
+                        const int64_t i0 = ir * D_MR;
+                        const int64_t mr = mc - i0 < D_MR ? mc - i0 : D_MR;
+                        dmicro_maxplus_f64(mr, nr, kc, pa + ir * D_MR * kc, pb + jr * D_NR * kc,
+                                           C + (ic + i0) * N + (jc + j0), N);
                     }
                 }
             }

@@ -70,9 +70,11 @@ def test_json_line(args):
         assert base["value"] > 0 and base["cores"] == 1 and base["kind"] in ("port", "reference")
         assert "argmax" in base["sample"]
         assert out["argmax_consistency_check"] is True
-    if args[1] == "F2":  # f64: against the FP64 vector peak; no CPU restatement, said so
+    if args[1] == "F2":  # f64: against the FP64 vector peak; the reference's AVX2 f64 path
         assert roof["unit"] == "TFLOP/s" and roof["peak"] == 78.6 and out["dtype"] == "f64"
-        assert "cpu_baseline" not in out and out["cpu_baseline_note"]
+        base = out["cpu_baseline"]
+        assert base["value"] > 0 and base["cores"] == 1 and base["kind"] == "port"
+        assert "F64_AVX2" in base["sample"]
     if args[1] == "C1":  # the reference's value-only CPU path on the same product
         base = out["cpu_baseline_value_only"]
         assert base["value"] > 0 and base["cores"] == 1 and "AVX2" in base["sample"]

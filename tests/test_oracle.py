@@ -229,6 +229,23 @@ def test_avx2_value_baseline_equals_oracle(sr):
                                                       "maxmul": 0.0}[sr], np.float32))
 
 
+def test_avx2_maxplus_f64_baseline_equals_oracle():
+    # 300 x 600 x 270 crosses every block edge of the 128/128/256 tiling and
+    # leaves partial 4 x 4 micro-blocks; values with ties across k (quarters).
+    rng = np.random.default_rng(14)
+    a = np.round(rng.standard_normal((300, 600)) * 4) / 4
+    b = np.round(rng.standard_normal((600, 270)) * 4) / 4
+    c1, _ = oracle.gemm("maxplus", a, b, with_argmax=False)
+    c2 = oracle.avx2_gemm_maxplus_f64("maxplus", a, b)
+    np.testing.assert_array_equal(tc.bits(c1), tc.bits(c2))
+    # Brute force on a corner: max over k of a[i, k] + b[k, j].
+    np.testing.assert_array_equal(c2[:5, :7], (a[:5, :, None] + b[None, :, :7]).max(axis=1))
+    z = oracle.avx2_gemm_maxplus_f64("maxplus", np.zeros((3, 0)), np.zeros((0, 5)))
+    np.testing.assert_array_equal(z, np.full((3, 5), -np.inf))
+    with pytest.raises(ValueError):
+        oracle.avx2_gemm_maxplus_f64("minplus", a, b)
+
+
 @pytest.mark.parametrize("sr", ["maxplus", "minplus", "maxmul"])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_oracle_nan_closed_forms(sr, dtype):
