@@ -133,6 +133,10 @@ def test_python_layer_rejects_host_tensors():
     ("maxplus", "f64", 64, 64, 640, True, "tiles_chunked"),
     ("maxplus", "f64", 4096, 4096, 4096, False, "dl64_4x8"),
     ("maxplus", "f64", 4096, 4096, 128, False, "tiles"),
+    ("maxplus", "f32", 2048, 2048, 2048, False, "dl_4x8"),           # E1's GEMMs: one 64x64 round
+    ("minplus", "f32", 2048, 4096, 1024, False, "dl_8x8_cl32"),      # one 128x128 round
+    ("maxplus", "f32", 3072, 3072, 2048, False, "dl_4x4_cl32"),      # 1.125 rounds of 128x128
+    ("maxplus", "f32", 1536, 2048, 2048, False, "dl_4x4_cl32"),      # 0.75 rounds of 64x64
 ])
 def test_gemm_plan_names_the_configured_paths(sr, dt, m, n, k, argmax, expected):
     if expected == "shortk":

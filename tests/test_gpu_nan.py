@@ -120,13 +120,15 @@ def test_nan_rule_per_path(sr, dt, m, n, k, argmax, api, path):
     assert_nan_exact(c, am, c_ref, am_ref if argmax else None)
 
 
-# The two large-tile paths at full tile counts; the oracle checks the rows
+# The large-tile paths at full tile counts; the oracle checks the rows
 # that hold NaN products plus a sample of the others (rows are independent).
 BIG = [
     ("maxplus", 6144, 2048, 544, True, "dl_4x8_cl16"),
     ("minplus", 6144, 2048, 544, True, "dl_4x8_cl16"),
     ("maxplus", 4096, 4096, 96, False, "dl_8x8_cl32"),
     ("maxmul", 4096, 4096, 64, False, "dl_8x8_cl32"),
+    ("maxplus", 2048, 2048, 96, False, "dl_4x8"),
+    ("maxmul", 1024, 4096, 64, False, "dl_4x8"),
 ]
 
 

@@ -332,6 +332,60 @@ def test_full_tile_shapes(sr, dt):
         assert_exact(c, None, c_ref, None)
 
 
+# Value-only tile shapes chosen by how the tiles fill the resident slots of
+# the 256 CUs: 64 x 128 tiles where 64 x 64 tiles would make exactly one
+# round (1024 tiles), 128 x 128 tiles for exactly one round of their own
+# (512 tiles).  The oracle checks a sample of rows (rows are independent).
+VALUE_TILE_CASES = [
+    ("maxplus", "f32", 2048, 2048, 256, "dl_4x8"),
+    ("minplus", "f32", 2000, 2048, 160, "dl_4x8"),  # partial last row tile
+    ("maxmul", "f32", 1024, 4096, 96, "dl_4x8"),
+    ("maxplus", "i32", 2048, 2048, 128, "dl_4x8"),
+    ("minplus", "i32", 2048, 2048, 256, "dl_4x8"),
+    ("maxmul", "i32", 1024, 4096, 64, "dl_4x8"),
+    ("minplus", "f32", 2048, 4096, 512, "dl_8x8_cl32"),
+]
+
+
+@pytest.mark.parametrize("sr,dt,m,n,k,path", VALUE_TILE_CASES,
+                         ids=[f"{c[0]}-{c[1]}-{c[2]}x{c[3]}x{c[4]}-{c[5]}" for c in VALUE_TILE_CASES])
+def test_value_only_tile_shapes(sr, dt, m, n, k, path):
+    nat = _nat()
+    assert nat.gemm_plan(sr, dt, m, n, k, False) == path
+    print(f"[case] value-only tiles {sr} {dt} {m}x{n}x{k} {path}", flush=True)
+    rng = np.random.default_rng(m + n + k)
+    dtype = tc.NP_DTYPES[dt]
+    a = tc.rng_matrix(rng, dtype, (m, k), -1000, 1000)
+    b = tc.rng_matrix(rng, dtype, (k, n), -1000, 1000)
+    c, _ = gpu_gemm(sr, a, b, False)
+    rows = np.unique(np.concatenate([np.arange(0, m, 61), [63, 64, m - 1]]))
+    c_ref, _ = oracle.gemm(sr, a[rows], b)
+    assert_exact(c[rows], None, c_ref, None)
+
+
+def test_value_only_wide_tiles_batched():
+    """Four 1024 x 1024 items make one round of 64 x 64 tiles together, so
+    the batch runs on 64 x 128 tiles (blockIdx.z per item)."""
+    from tropical_gemm import ops
+
+    nat = _nat()
+    batch, m, n, k = 4, 1024, 1024, 256
+    assert nat.gemm_plan("maxplus", "f32", m, n, k, False, batch=batch,
+                         strides=(m * k, k * n, m * n)) == "dl_4x8"
+    rng = np.random.default_rng(404)
+    a = np.round(rng.standard_normal((batch, m, k)) * 4).astype(np.float32) / 4 + 0.0625
+    b = np.round(rng.standard_normal((batch, k, n)) * 4).astype(np.float32) / 4 + 0.0625
+    print("[case] value-only 64x128 tiles, batch 4", flush=True)
+    c, _ = ops.gemm_batched("maxplus", torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV),
+                            False)
+    torch.cuda.synchronize()
+    c = c.cpu().numpy()
+    rows = np.array([0, 1, 63, 64, 500, m - 1])
+    for z in range(batch):
+        c_ref, _ = oracle.gemm("maxplus", a[z][rows], b[z])
+        np.testing.assert_array_equal(tc.bits(c[z][rows]), tc.bits(c_ref))
+
+
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
 @pytest.mark.parametrize("dt", ["f32", "i32"])
 @pytest.mark.parametrize("k", [96, 320, 1056])

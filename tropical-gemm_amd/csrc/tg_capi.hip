@@ -584,7 +584,7 @@ constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
 // The kernel a problem runs on.
-enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_44_8, DL_44_16, DL_44_32, DL64, DL64_VALUE, TILES_EXACT, TILES_CHUNKED, TILES };
+enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_48_VALUE, DL_44_8, DL_44_16, DL_44_32, DL64, DL64_VALUE, TILES_EXACT, TILES_CHUNKED, TILES };
 
 struct Plan {
     Path path = Path::TILES;
@@ -666,11 +666,24 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             const bool wide = splits == 1 && argmax && cl == 16 && p.N % W48::BN == 0 &&
                               p.K % W48::BK == 0 &&
                               ((p.M + W48::BM - 1) / W48::BM) * (p.N / W48::BN) * p.batch >= 1536;
-            // Value-only problems with at least two rounds of 128 x 128 tiles
-            // (512 resident workgroups) run 8 x 8 outputs per thread.
+            // Value-only tile shape by how the tiles fill the resident slots
+            // of the 256 CUs (128 x 128 tiles run two per CU, 512 slots;
+            // 64 x 64 tiles four, 1024 slots).  128 x 128 tiles (8 x 8
+            // outputs per thread) from two rounds up, or exactly one round
+            // (2048 x 4096 x 1024: 241 against 267-279 us for 64 x 64; one
+            // and a bit rounds, 3072^2 x 2048, take 855 against 593-628 us);
+            // 64 x 128 tiles where 64 x 64 would make exactly one round
+            // (2048^2 x 2048: 265-269 against 286-290 us; 5-8% at K = 1024 ..
+            // 4096); 64 x 64 otherwise (0.75 or 1.25 rounds: 5-15% faster
+            // than 64 x 128).
+            constexpr int64_t kCus = 256;
+            const int64_t t128 =
+                ((p.M + W88::BM - 1) / W88::BM) * ((p.N + W88::BN - 1) / W88::BN) * p.batch;
+            const int64_t t64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.batch;
             const bool big = splits == 1 && !argmax && p.K % W88::BK == 0 &&
-                             ((p.M + W88::BM - 1) / W88::BM) * ((p.N + W88::BN - 1) / W88::BN) *
-                                     p.batch >= 1024;
+                             (t128 >= 4 * kCus || t128 == 2 * kCus);
+            const bool mid = splits == 1 && !argmax && !big && t64 == 4 * kCus &&
+                             p.N % W48::BN == 0 && p.K % W48::BK == 0;
             pl.splits = splits;
             if (wide && tg::dl_fits<16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
                 pl.path = Path::DL_48_16;
@@ -679,6 +692,11 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
             }
             if (big && tg::dl_fits<32>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
                 pl.path = Path::DL_88_32;
+                pl.splits = 1;
+                return pl;
+            }
+            if (mid && tg::dl_fits<16>(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::DL_48_VALUE;
                 pl.splits = 1;
                 return pl;
             }
@@ -737,6 +755,7 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
             case Path::KRES: return run_gemm_kres<SR, T>(p, st);
             case Path::DL_88_32: return run_gemm_dl<SR, T, 8, 8, 32>(p, ws, 1, st);
             case Path::DL_48_16: return run_gemm_dl<SR, T, 4, 8, 16>(p, ws, 1, st);
+            case Path::DL_48_VALUE: return run_gemm_dl<SR, T, 4, 8, 16>(p, ws, 1, st);  // CL unused
             case Path::DL_44_8: return run_gemm_dl<SR, T, 4, 4, 8>(p, ws, pl.splits, st);
             case Path::DL_44_16: return run_gemm_dl<SR, T, 4, 4, 16>(p, ws, pl.splits, st);
             case Path::DL_44_32: return run_gemm_dl<SR, T, 4, 4, 32>(p, ws, pl.splits, st);
@@ -848,6 +867,7 @@ const char* path_name(Path path) {
         case Path::KRES: return "kres";
         case Path::DL_88_32: return "dl_8x8_cl32";
         case Path::DL_48_16: return "dl_4x8_cl16";
+        case Path::DL_48_VALUE: return "dl_4x8";
         case Path::DL_44_8: return "dl_4x4_cl8";
         case Path::DL_44_16: return "dl_4x4_cl16";
         case Path::DL_44_32: return "dl_4x4_cl32";
