@@ -77,7 +77,7 @@ KERNEL_NAMES = {
 # profiles/tg_gemm_dl_split_*.md, profiles/tg_gemm_dl64_*.md).  E1: per GEMM
 # launch; C1: the split GEMM launch (the merge adds 0.025e9).
 
-TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.052e9,
+TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.042e9,
            "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9}
 
 

@@ -323,7 +323,12 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     const int64_t MN = p.M * p.N;
     const int64_t sY = splits > 1 ? p.batch * MN : 0;
     const int64_t KS = p.K / splits;
-    if (argmax) {  // B^T staging for the resolve, outside the timed GEMM launches
+    // Split-K problems are small: when all of B (every batch item) fits in
+    // 4 MiB it stays in L2, and the resolve reads B's columns directly
+    // (BDIRECT), with no B^T staged and one launch fewer.
+    const bool bdirect = argmax && splits > 1 && TN == 4 && p.K % Cfg::BK == 0 &&
+                         size_t(p.batch) * size_t(p.K) * size_t(p.N) * sizeof(T) <= (size_t(4) << 20);
+    if (argmax && !bdirect) {  // B^T staging for the resolve, outside the timed GEMM launches
         if ((p.K + 31) / 32 > 65535)
             return fail(TG_ERR_DIMENSION_MISMATCH, "K too large for the transpose grid");
         for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
@@ -354,6 +359,16 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         const bool tailk = p.K % Cfg::BK != 0;  // the last k-tile is partial
         if (argmax) {
             const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
+            if constexpr (TM == 4 && TN == 4 && (Cfg::BK / CL) % 2 == 0) {
+                if (bdirect) {
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, true>), grid,
+                                       dim3(256), Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz, Iz, p.M,
+                                       p.N, p.K, p.sA, p.sB, sCk, int(tiles_m), int(tiles_n), KS,
+                                       sY);
+                    TG_HIP(hipGetLastError());
+                    continue;
+                }
+            }
             if constexpr (TM == 4 && (Cfg::BK / CL) % 2 == 0) {
                 if (tailk) {
                     // 64 x 64 tiles only: the 64 x 128 kernel with the tail
@@ -394,7 +409,7 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
         const int64_t nvec = p.batch * MN / 4;
         int64_t blocks = (nvec + 255) / 256;
         if (blocks > 8192) blocks = 8192;
-        const T* BT = argmax ? reinterpret_cast<const T*>(wsb + wl.bt) : nullptr;
+        const T* BT = argmax && !bdirect ? reinterpret_cast<const T*>(wsb + wl.bt) : nullptr;
         if (argmax)
             hipLaunchKernelGGL((tg::tg_merge_splits<SR, T, true>), dim3(unsigned(blocks)), dim3(256), 0,
                                st, PV, PI, C, p.IDX, splits, MN, p.batch, sY, p.sC, A, B, BT, p.N,

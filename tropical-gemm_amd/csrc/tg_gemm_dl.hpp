@@ -176,9 +176,9 @@ __global__ __launch_bounds__(256) void tg_merge_splits(const T* __restrict__ PV,
                 const int64_t i = (r + q) / N, j = (r + q) - ((r + q) / N) * N;
                 const T* a = A + z * sA + i * K;
                 int32_t ix;
-                if constexpr (ARGMAX)
+                if (ARGMAX && BT != nullptr)
                     cpu_select<SR, T>(a, 1, BT + z * (N * K) + j * K, 1, K, best.v[q], ix);
-                else
+                else  // value-only, or argmax resolved from B (no B^T staged)
                     cpu_select<SR, T>(a, 1, B + z * sB + j, N, K, best.v[q], ix);
                 if constexpr (ARGMAX) bi.v[q] = ix;
             }
@@ -225,7 +225,12 @@ __device__ __forceinline__ void record4(int32_t& c0, int32_t& c1, int32_t& c2, i
 // waves hide the LDS latency of the main loop.
 // TAILK: K is not a multiple of BK (the last k-tile is partial); a separate
 // instantiation, so full-K problems run the plain pipeline.
-template <int SR, typename T, bool ARGMAX, int TM_, int TN_, int CL, bool TAILK = false>
+// BDIRECT (argmax): the resolve reads each window's B values down B's column
+// (CL loads with stride N) instead of from a staged B^T row, and BT is
+// unused; for split-K problems whose B stays in L2 (the host decides), where
+// it saves the transpose launch (1024^3: 68 against 71 us per call).
+template <int SR, typename T, bool ARGMAX, int TM_, int TN_, int CL, bool TAILK = false,
+          bool BDIRECT = false>
 __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     ARGMAX ? DlCfg<TM_, TN_>::WAVES_ARGMAX : DlCfg<TM_, TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
@@ -261,7 +266,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     C += z * sC + y * sY;
     if (ARGMAX) {
         IDX += z * sC + y * sY;
-        BT += z * (N * K);
+        if constexpr (!BDIRECT) BT += z * (N * K);
     }
     // Tile row / column of this thread's output (i, j).
     auto trow = [&](int i) { return (i >> 2) * 64 + ty * 4 + (i & 3); };
@@ -492,7 +497,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             if (split || gr >= M || gc >= N) continue;
             T v;
             int32_t ix;
-            if (argmax_out)
+            if (argmax_out && !BDIRECT)
                 cpu_select<SR, T>(A + gr * K, 1, BT + gc * K, 1, K, v, ix);
             else
                 cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
@@ -582,7 +587,9 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             // stored; their windows just stay in bounds).
             const int64_t gr = row0 + lid / BN, gc = col0 + (lid & (BN - 1));
             ap = A + (gr < M ? gr : M - 1) * K + c * CL;
-            bp = BT + (gc < N ? gc : N - 1) * K + c * CL;
+            // BDIRECT: bp is the window's first element in B's column (stride N).
+            bp = BDIRECT ? B + c * CL * N + (gc < N ? gc : N - 1)
+                         : BT + (gc < N ? gc : N - 1) * K + c * CL;
             return c;
         };
         auto load_window = [&](int e, Window& wv) {
@@ -596,7 +603,12 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 // match is a k < K.
                 const int64_t off = (!TAILK || c * CL + w * 4 <= K - 4) ? w * 4 : K - 4 - c * CL;
                 wv.a[w] = *reinterpret_cast<const Vec16<T>*>(ap + off);
-                wv.b[w] = *reinterpret_cast<const Vec16<T>*>(bp + off);
+                if constexpr (BDIRECT) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) wv.b[w].v[q] = bp[(off + q) * N];
+                } else {
+                    wv.b[w] = *reinterpret_cast<const Vec16<T>*>(bp + off);
+                }
             }
         };
         if (tid < total) {
@@ -628,7 +640,8 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                         const T* ap;
                         const T* bp;
                         window_ptrs(e, ap, bp);
-                        if (__builtin_signbit(tmul<SR, T>(ap[f], bp[f]))) r |= 32;
+                        const T bf = BDIRECT ? bp[int64_t(f) * N] : bp[f];
+                        if (__builtin_signbit(tmul<SR, T>(ap[f], bf))) r |= 32;
                     }
                 }
                 chs[int(list[e])] = uint16_t(r);
