@@ -178,6 +178,15 @@ int tg_gemm_noalloc(int device, tg_semiring semiring, tg_dtype dtype, tg_layout 
                     const void* A, const void* B, void* C, int32_t* argmax,
                     int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Bytes of the fixed scratch array tg_gemm_noalloc would use for this
+ * problem (0 when its kernel reads no workspace); a call whose need is above
+ * TG_NOALLOC_SCRATCH_BYTES is rejected.  (size_t)-1 for arguments the call
+ * would reject.  Pure host logic, as tg_gemm_plan (pointers are checked for
+ * alignment only).  Diagnostic, with no counterpart in the reference. */
+size_t tg_gemm_noalloc_bytes(tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                             const void* A, const void* B, const void* C, const int32_t* argmax,
+                             int64_t m, int64_t n, int64_t k);
+
 /*
  * Strided batched product: C[t] = A[t] (x) B[t] for t < batch, element
  * strides between consecutive matrices.  Replaces
@@ -205,14 +214,18 @@ int tg_gemm_strided_batched_ws(int device, tg_semiring semiring, tg_dtype dtype,
  * Replaces tropical_backward_a_gpu_kernel + kernel tropical_backward_a_{f32,f64}
  * (crates/tropical-gemm-cuda/src/lib.rs:841-882, tropical_gemm.cu:1002-1018) and
  * the torch scatter_add_ backward (pytorch.py:386-403).  Float dtypes only.
- * Accumulation order across j is not fixed (f32 tolerance, see docs).
+ * Deterministic: every element is summed from +0 in ascending j, the order of
+ * the reference CPU loop (crates/tropical-gemm/src/api.rs:563-582), so the
+ * result is bit-identical to it and to every other run.  m == 0 or n == 0
+ * (grad_c and argmax may then be NULL) gives an all-(+0) gradient.
  */
 int tg_backward_a(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
                   const int32_t* argmax, void* grad_a, int64_t m, int64_t n, int64_t k,
                   void* stream);
 
 /* grad_b[argmax[i,j], j] += grad_c[i,j]; grad_b (k x n) fully overwritten.
- * Replaces tropical_backward_b_gpu_kernel (lib.rs:901-942, .cu:1020-1036). */
+ * Replaces tropical_backward_b_gpu_kernel (lib.rs:901-942, .cu:1020-1036).
+ * Summed from +0 in ascending i (api.rs:627-646): bit-identical, deterministic. */
 int tg_backward_b(int device, tg_dtype dtype, tg_layout layout, const void* grad_c,
                   const int32_t* argmax, void* grad_b, int64_t m, int64_t n, int64_t k,
                   void* stream);

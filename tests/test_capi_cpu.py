@@ -168,3 +168,41 @@ def test_backward_geometry_caps_every_launch_dimension(dt, want_a, shape):
         elem = 4 if dt == 0 else 8
         if k * elem > 128 * 1024:
             assert "global" in plan, plan
+
+
+def _noalloc_bytes(sr, dt, m, n, k, argmax, layout="row"):
+    lib = nat.load()
+    return lib.tg_gemm_noalloc_bytes(nat.SEMIRING[sr], nat.DTYPE[dt], nat.LAYOUT[layout], 256, 256,
+                                     256, 256 if argmax else None, m, n, k)
+
+
+def _round256(x):
+    return -(-x // 256) * 256
+
+
+@pytest.mark.parametrize("m,n,k,argmax", [(2048, 2048, 1024, True), (2048, 2048, 1024, False),
+                                          (1024, 2048, 512, False), (2000, 4004, 544, True)])
+def test_noalloc_bytes_cover_the_f64_direct_to_lds_workspace(m, n, k, argmax):
+    """f64 problems on the direct-to-LDS kernel read B^T (argmax) and the
+    operand classes (4 bytes per row of A and per column of B) from the
+    workspace: tg_gemm_noalloc's scratch need counts both."""
+    plan = nat.gemm_plan("maxplus", "f64", m, n, k, argmax, workspace_bytes=64 << 20)
+    assert plan.startswith("dl64"), plan
+    want = (_round256(k * n * 8) if argmax else 0) + _round256((m + n) * 4)
+    assert _noalloc_bytes("maxplus", "f64", m, n, k, argmax) == want
+
+
+def test_noalloc_bytes_of_other_paths():
+    # 32-bit argmax on the direct-to-LDS kernel: B^T staging (row-major: k x n).
+    assert nat.gemm_plan("maxplus", "f32", 4096, 4096, 4096, True) == "dl_4x8_cl16"
+    assert _noalloc_bytes("maxplus", "f32", 4096, 4096, 4096, True) == 4096 * 4096 * 4
+    # Split K: the value and index partials after the (here unused) B^T region.
+    assert nat.gemm_plan("maxplus", "f32", 1024, 1024, 1024, True,
+                         workspace_bytes=64 << 20) == "dl_4x4_cl8 split 2"
+    assert _noalloc_bytes("maxplus", "f32", 1024, 1024, 1024, True) == \
+        1024 * 1024 * 4 + 2 * (2 * 1024 * 1024 * 4)
+    # Paths without workspace, and empty products.
+    assert _noalloc_bytes("maxplus", "f32", 4096, 4096, 4096, False) == 0
+    assert _noalloc_bytes("maxplus", "i32", 262144, 128, 128, True) == 0
+    assert _noalloc_bytes("maxplus", "f32", 0, 4, 4, True) == 0
+    assert _noalloc_bytes("maxplus", "f32", -1, 4, 4, True) == 2**64 - 1

@@ -112,6 +112,55 @@ def test_backward_column_major_and_out_of_range_index():
     assert_bits(gb.cpu().numpy().reshape(n, k).T, ref_b)
 
 
+# Products with no rows or no columns: every gradient element has no
+# contribution, so each gradient comes back all +0 (the reference's zeroed
+# output, api.rs:563-582), with NULL grad_c / argmax (and NULL `other`)
+# accepted.  The scatter kernels must not run: their first clamped read would
+# be at index -1.
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("mult", [False, True])
+@pytest.mark.parametrize("shape", [(37, 0, 29), (0, 23, 29)])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_backward_empty_product(dtype, mult, shape, layout):
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    m, n, k = shape
+    dt = 0 if dtype == np.float32 else 1
+    print(f"[case] backward empty m={m} n={n} k={k} {np.dtype(dtype).name} mult={mult} layout={layout}",
+          flush=True)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    tdt = torch.float32 if dtype == np.float32 else torch.float64
+    for want_a, elems in ((True, m * k), (False, k * n)):
+        if elems == 0:
+            continue
+        out = torch.full((elems + 8,), float("nan"), dtype=tdt, device=DEV)
+        if mult:
+            fn = lib.tg_maxmul_backward_a if want_a else lib.tg_maxmul_backward_b
+            nat.check(fn(0, dt, layout, None, None, None, p(out), m, n, k, None))
+        else:
+            fn = lib.tg_backward_a if want_a else lib.tg_backward_b
+            nat.check(fn(0, dt, layout, None, None, p(out), m, n, k, None))
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert_bits(got[:elems], np.zeros(elems, dtype))
+        assert np.all(np.isnan(got[elems:])), "wrote past the gradient"
+    # Strided batches with gaps: every matrix zeroed, the gaps untouched.
+    batch = 3
+    for want_a, elems in ((True, m * k), (False, k * n)):
+        if elems == 0:
+            continue
+        stride = elems + 5
+        out = torch.full((batch * stride,), float("nan"), dtype=tdt, device=DEV)
+        fn = lib.tg_backward_a_strided_batched if want_a else lib.tg_backward_b_strided_batched
+        nat.check(fn(0, dt, layout, None, None, None, p(out), batch, m, n, k, m * n,
+                     k * n if want_a else m * k, stride, None))
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(batch, stride)
+        assert_bits(got[:, :elems], np.zeros((batch, elems), dtype))
+        assert np.all(np.isnan(got[:, elems:]))
+
+
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
 def test_batched_backward(sr):
     from tropical_gemm import ops

@@ -240,3 +240,64 @@ def test_backward_fuzz(seed):
             # The kernels add in the reference's order: the same bits.
             np.testing.assert_array_equal(tc.bits(np.ascontiguousarray(ot)),
                                           tc.bits(np.ascontiguousarray(ref)))
+
+
+# The wide-tile paths (128 x 128 value-only, 64 x 128 value-only and argmax,
+# the f64 direct-to-LDS kernel) on shapes whose last row and column tiles are
+# partial, each planned onto its path (tg_gemm_plan), with guard bytes around
+# C, argmax and the workspace, and sampled rows (edge tiles included) against
+# the oracle.
+WIDE_CASES = [
+    ("maxplus", "f32", 2000, 4000, 256, False, "dl_8x8_cl32"),
+    ("minplus", "i32", 2000, 4000, 256, False, "dl_8x8_cl32"),
+    ("maxmul", "f32", 2000, 2048, 160, False, "dl_4x8"),
+    ("maxplus", "f32", 4090, 4096, 1024, True, "dl_4x8_cl16"),
+    ("minplus", "f64", 2000, 4004, 512, False, "dl64_4x8"),
+    ("maxplus", "f64", 2000, 4004, 544, True, "dl64_4x8_cl16"),
+]
+
+
+@pytest.mark.parametrize("sr,dt,m,n,k,with_argmax,path", WIDE_CASES,
+                         ids=[f"{c[6]}-{c[0]}-{c[1]}-{c[2]}x{c[3]}x{c[4]}" for c in WIDE_CASES])
+def test_wide_paths_guarded(sr, dt, m, n, k, with_argmax, path):
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    assert nat.gemm_plan(sr, dt, m, n, k, with_argmax) == path
+    print(f"[case] guarded {path} {sr} {dt} {m}x{n}x{k} argmax={with_argmax}", flush=True)
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    if dt in ("f32", "f64"):
+        a = rng.standard_normal((m, k)).astype(NP[dt])
+        b = rng.standard_normal((k, n)).astype(NP[dt])
+        if sr == "maxmul":
+            a, b = np.abs(a), np.abs(b)
+    else:
+        a = rng.integers(-1000, 1001, size=(m, k)).astype(NP[dt])
+        b = rng.integers(-1000, 1001, size=(k, n)).astype(NP[dt])
+    es = np.dtype(NP[dt]).itemsize
+    ta, tb = torch.from_numpy(a).to(DEV), torch.from_numpy(b).to(DEV)
+    c_bytes, i_bytes = m * n * es, m * n * 4
+    cbuf = _guarded(c_bytes)
+    ibuf = _guarded(i_bytes) if with_argmax else None
+    ws_bytes = lib.tg_gemm_workspace_size(nat.DTYPE[dt], 1, m, n, k, int(with_argmax))
+    wbuf = _guarded(ws_bytes + 256)
+    woff = GUARD + (-(wbuf.data_ptr() + GUARD)) % 256
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.check(lib.tg_gemm_ws(0, nat.SEMIRING[sr], nat.DTYPE[dt], nat.LAYOUT["row"], _p(ta), _p(tb),
+                             _p(cbuf, GUARD), _p(ibuf, GUARD) if with_argmax else None, m, n, k,
+                             _p(wbuf, woff), ws_bytes, stream))
+    torch.cuda.synchronize()
+    assert _guards_ok(cbuf, c_bytes), "C guard overwritten"
+    if with_argmax:
+        assert _guards_ok(ibuf, i_bytes), "argmax guard overwritten"
+    assert bool(torch.all(wbuf[:woff] == FILL)) and bool(torch.all(wbuf[woff + ws_bytes:] == FILL)), \
+        "workspace overrun"
+    c = cbuf[GUARD:GUARD + c_bytes].cpu().numpy().view(NP[dt]).reshape(m, n)
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), [63, 64, 127, 128, m - 2, m - 1]]))
+    c_ref, am_ref = oracle.gemm(sr, a[rows], b, with_argmax=with_argmax)
+    if with_argmax:
+        am = ibuf[GUARD:GUARD + i_bytes].cpu().numpy().view(np.int32).reshape(m, n)
+        np.testing.assert_array_equal(tc.bits(c[rows]), tc.bits(c_ref))
+        np.testing.assert_array_equal(am[rows].astype(np.int64), am_ref.astype(np.int64))
+    else:
+        np.testing.assert_array_equal(c[rows], c_ref)

@@ -344,6 +344,7 @@ VALUE_TILE_CASES = [
     ("minplus", "i32", 2048, 2048, 256, "dl_4x8"),
     ("maxmul", "i32", 1024, 4096, 64, "dl_4x8"),
     ("minplus", "f32", 2048, 4096, 512, "dl_8x8_cl32"),
+    ("maxplus", "f32", 2000, 4000, 256, "dl_8x8_cl32"),  # partial row and column tiles
 ]
 
 

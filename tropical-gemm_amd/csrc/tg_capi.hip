@@ -1074,6 +1074,10 @@ int scratch_address(int device, void** out) {
 size_t scratch_need(tg_dtype dt, const Problem& p, const Plan& pl) {
     const bool argmax = p.IDX != nullptr;
     if (!uses_workspace(pl, argmax)) return 0;
+    // The f64 direct-to-LDS kernel's workspace: B^T (argmax) and the operand
+    // classes of A's rows and B's columns (run_gemm_dl64).
+    if (pl.path == Path::DL64 || pl.path == Path::DL64_VALUE)
+        return dl64_ws_bytes(p.batch, p.M, p.N, p.K, argmax);
     return ws_layout(dt, p.batch, p.M, p.N, p.K, argmax, pl.splits).total;
 }
 
@@ -1154,9 +1158,25 @@ int allow_lds(K* kernel, size_t bytes) {
     return TG_OK;
 }
 
+// A gradient with no contributions (the product has no rows or no columns):
+// `batch` matrices of len elements, stride apart, all +0.  The scatter
+// kernels would read their first (clamped) contribution at index -1.
+template <typename T>
+int zero_gradient(T* out, int64_t len, int64_t batch, int64_t stride, hipStream_t st) {
+    const int64_t total = len * batch;
+    if (total == 0) return TG_OK;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL((tg::tg_fill_zero_runs<T>), dim3(unsigned(blocks)), dim3(256), 0, st, out,
+                       len, batch, stride);
+    TG_HIP(hipGetLastError());
+    return TG_OK;
+}
+
 template <typename T, bool MULT>
 int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sA, hipStream_t st) {
+    if (N == 0) return zero_gradient(GA, M * K, batch, sA, st);
     const BwdGeometry g = bwd_rows_geometry(batch * M, K, sizeof(T));
     if (g.grid == 0) return TG_OK;
     if (g.global) {
@@ -1177,6 +1197,7 @@ int run_backward_rows(const T* G, const int32_t* I, const T* O, T* GA, int64_t b
 template <typename T, bool MULT>
 int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sB, hipStream_t st) {
+    if (M == 0) return zero_gradient(GB, K * N, batch, sB, st);
     const BwdGeometry g = bwd_cols_geometry(batch, N, K, sizeof(T));
     if (g.grid == 0) return TG_OK;
     if (g.global) {
@@ -1448,6 +1469,17 @@ int tg_gemm_noalloc(int device, tg_semiring semiring, tg_dtype dtype, tg_layout 
     rc = scratch_address(device, &ws);
     if (rc != TG_OK) return rc;
     return run_gemm(semiring, dtype, p, ws, kScratchBytes, as_stream(stream));
+}
+
+size_t tg_gemm_noalloc_bytes(tg_semiring semiring, tg_dtype dtype, tg_layout layout,
+                             const void* A, const void* B, const void* C, const int32_t* argmax,
+                             int64_t m, int64_t n, int64_t k) {
+    if (validate_forward(semiring, dtype, layout, A, B, C, 1, m, n, k, 0, 0, 0, false) != TG_OK)
+        return ~size_t(0);
+    if (m == 0 || n == 0) return 0;
+    const Problem p = make_problem(layout, A, B, const_cast<void*>(C), const_cast<int32_t*>(argmax),
+                                   1, m, n, k, 0, 0, 0, false);
+    return scratch_need(dtype, p, plan_gemm(semiring, dtype, p, kScratchBytes));
 }
 
 size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t n, int64_t k,

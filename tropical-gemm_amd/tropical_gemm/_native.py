@@ -54,6 +54,7 @@ SIGNATURES = {
     "tg_kernel_timing_read": ([ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)], _i32),
     "tg_gemm": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp], _i32),
     "tg_gemm_noalloc": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp], _i32),
+    "tg_gemm_noalloc_bytes": ([_i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64], _sz),
     "tg_gemm_workspace_size": ([_i32, _i64, _i64, _i64, _i64, _i32], _sz),
     "tg_gemm_ws": ([_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp],
                    _i32),
