@@ -340,11 +340,20 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     }
     // 128 x 128 value-only tiles take 64 KB of dynamic LDS: raise the
     // kernel's limit once (no stream work, so also fine under capture).
+    // The value-only 8 x 8 tiles run the pipelined main loop (tg::pipe_fits).
+    constexpr bool kPipe = TM == 8 && TN == 8;
+    const bool pipe = kPipe && !argmax && tg::pipe_fits(p.N, p.K);
     if constexpr (Cfg::TILE_BYTES > 48 * 1024) {
         static const hipError_t attr = hipFuncSetAttribute(
             reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, false, TM, TN, CL>),
             hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::TILE_BYTES);
         TG_HIP(attr);
+        if constexpr (kPipe) {
+            static const hipError_t attr_pipe = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, false, TM, TN, CL, false, false, 2>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::TILE_BYTES);
+            TG_HIP(attr_pipe);
+        }
     }
     KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
@@ -398,6 +407,12 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
                                        int(tiles_n), KS, sY);
                 else
                     return fail(TG_ERR_INVALID_ARGUMENT, "internal: wide tiles need K % 32 == 0");
+            } else if (pipe) {
+                if constexpr (kPipe)
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TM, TN, CL, false, false, 2>),
+                                       grid, dim3(256), Cfg::TILE_BYTES, st, Az, Bz, nullptr, Cz,
+                                       nullptr, p.M, p.N, p.K, p.sA, p.sB, sCk, int(tiles_m),
+                                       int(tiles_n), KS, sY);
             } else
                 hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, false, TM, TN, CL>), grid, dim3(256),
                                    Cfg::TILE_BYTES, st, Az, Bz, nullptr, Cz, nullptr, p.M, p.N,

@@ -18,6 +18,8 @@
 // 4 x 8, 1 for 8 x 8).
 #pragma once
 
+#include <utility>
+
 #include "tg_kernels.hpp"
 
 namespace tg {
@@ -88,6 +90,63 @@ __device__ __forceinline__ void lds_load16(const void* src, void* dst) {
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
+// Byte address of a pointer into LDS, as ds_* instructions take it (the low
+// 32 bits of the generic address are the offset in the LDS aperture).
+__device__ __forceinline__ uint32_t lds_byte_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
+}
+
+// A 16-byte LDS read issued without a wait: the caller waits for it with
+// lds_wait before it uses r.  The compiler does not track these reads, so
+// nothing else may read r in between.
+template <int OFF, typename V>
+__device__ __forceinline__ void lds_read16_nowait(V& r, uint32_t addr) {
+    static_assert(sizeof(V) == 16 && OFF >= 0 && OFF < 65536, "ds_read_b128, 16-bit offset");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+}
+
+template <int OFF, typename V>
+__device__ __forceinline__ void lds_read8_nowait(V& r, uint32_t addr) {
+    static_assert(sizeof(V) == 8 && OFF >= 0 && OFF < 65536, "ds_read_b64, 16-bit offset");
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+}
+
+// Waits for every outstanding LDS read of this wave; the values of the
+// registers read into (tied here) are only used after it.
+// lds_wait<N>: waits until at most N of this wave's LDS reads are
+// outstanding (LDS reads complete in order, so the older ones are done; a
+// scalar load in flight only makes the wait stricter).
+template <int N = 0, typename V>
+__device__ __forceinline__ void lds_wait(V& r0, V& r1, V& r2, V& r3) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3) : "i"(N) : "memory");
+}
+template <int N = 0, typename V, typename W>
+__device__ __forceinline__ void lds_wait(V& r0, V& r1, V& r2, V& r3, W& r4, W& r5, W& r6, W& r7) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), "+v"(r4), "+v"(r5), "+v"(r6), "+v"(r7)
+                 : "i"(N)
+                 : "memory");
+}
+
+// An empty asm statement that uses x: the values are computed before it (and
+// so before every later asm statement, which keeps its order).
+template <typename T>
+__device__ __forceinline__ void pin8(const T& x0, const T& x1, const T& x2, const T& x3, const T& x4,
+                                     const T& x5, const T& x6, const T& x7) {
+    asm volatile("" ::"v"(x0), "v"(x1), "v"(x2), "v"(x3), "v"(x4), "v"(x5), "v"(x6), "v"(x7));
+}
+
+// f(std::integral_constant<int, I>{}) for I = 0 .. N-1, in order: the body
+// sees I as a constant expression (immediate LDS offsets, unrolled chunks).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // True when tg_gemm_dl<.., CL> can run the problem: K and N multiples of
 // 4 and 16-byte aligned operands, outputs and batch strides (tiles load and
 // store 16 bytes per lane), and chunk indices that fit the epilogue's 16-bit
@@ -103,6 +162,13 @@ inline bool dl_fits(int64_t M, int64_t N, int64_t K, int64_t sA, int64_t sB, int
     return M > 0 && N > 0 && K > 0 && N % 4 == 0 && K % 4 == 0 && (K + CL - 1) / CL < 0xFFFF &&
            K < (int64_t(1) << 26) && N < (int64_t(1) << 28) && sA % 4 == 0 && sB % 4 == 0 && sC % 4 == 0 && a16(A) && a16(B) && a16(C) &&
            (IDX == nullptr || a16(IDX));
+}
+
+// True when the pipelined value-only 8 x 8 main loop (PIPE) can run the
+// problem: its per-lane load offsets (up to 127 rows of A, 32 k rows of B)
+// fit 32 bits.
+inline bool pipe_fits(int64_t N, int64_t K) {
+    return K < (int64_t(1) << 23) && N < (int64_t(1) << 25);
 }
 
 // True when every tile of the problem is full.
@@ -229,10 +295,15 @@ __device__ __forceinline__ void record4(int32_t& c0, int32_t& c1, int32_t& c2, i
 // (CL loads with stride N) instead of from a staged B^T row, and BT is
 // unused; for split-K problems whose B stays in L2 (the host decides), where
 // it saves the transpose launch (1024^3: 68 against 71 us per call).
+// PIPE (value-only 8 x 8 outputs, whole k-tiles; its value is the waves per
+// SIMD the kernel is built for, 2): the fragments of the next k pair are
+// read from LDS while the current pair is folded (reads issued ahead and
+// waited for explicitly), so a wave does not stall on LDS between pairs
+// (MaxPlus f32 4096^3 on MI355X: 1.847 against 1.891 ms).
 template <int SR, typename T, bool ARGMAX, int TM_, int TN_, int CL, bool TAILK = false,
-          bool BDIRECT = false>
+          bool BDIRECT = false, int PIPE = 0>
 __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
-    ARGMAX ? DlCfg<TM_, TN_>::WAVES_ARGMAX : DlCfg<TM_, TN_>::WAVES_VALUE))) void tg_gemm_dl(
+    PIPE != 0 ? PIPE : ARGMAX ? DlCfg<TM_, TN_>::WAVES_ARGMAX : DlCfg<TM_, TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
     int64_t sB, int64_t sC, int tiles_m, int tiles_n, int64_t KS, int64_t sY) {
@@ -425,6 +496,155 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     const int64_t t0 = y * (KS / BK);
     const int64_t t1 = t0 + (KS + BK - 1) / BK;
     const int kv = TAILK ? int(KS - (t1 - 1 - t0) * BK) : BK;
+    if constexpr (PIPE != 0) {
+        static_assert(TM == 8 && TN == 8 && !TAILK && !ARGMAX,
+                      "pipelined main loop: value-only 8 x 8 outputs, whole k-tiles");
+        typedef T V4 __attribute__((ext_vector_type(4)));
+        typedef T V2 __attribute__((ext_vector_type(2)));
+        // Per-thread LDS byte addresses in buffer 0.  A: row trow(i) at
+        // a_thr + 128 (i & 3) + 64 * 128 (i >> 2); its k quad kq at the
+        // swizzled position (kq ^ swz) << 4 (row starts are 128-byte
+        // aligned, so the XOR touches only the quad bits).  B: k row at
+        // +512 k, this thread's column quads at +16 tx and +256 + 16 tx.
+        const uint32_t lds0 = lds_byte_addr(dl_lds);
+        const uint32_t a_thr = lds0 + uint32_t(ty) * (4 * BK * 4);
+        const uint32_t b_thr = lds0 + 2 * Cfg::A_BYTES + uint32_t(tx) * 16;
+        const uint32_t sw16 = uint32_t(ty & 7) << 4;
+        // Global -> LDS loads of k-tile t: wave-uniform base pointers advanced
+        // by a constant per tile, plus per-lane 32-bit byte offsets fixed for
+        // the whole loop (the row and column clamps of partial tiles
+        // included; they fit 32 bits by pipe_fits).
+        uint32_t poffA[NAI], poffB[NBI];
+#pragma unroll
+        for (int q = 0; q < NAI; ++q) {
+            const int r = (wave * NAI + q) * 8 + (lane >> 3);
+            const int64_t gr = row0 + r < M ? row0 + r : M - 1;
+            const int qsrc = (lane & 7) ^ ((r >> 2) & 7);
+            poffA[q] = uint32_t((gr - row0) * K * 4 + qsrc * 16);
+        }
+#pragma unroll
+        for (int q = 0; q < NBI; ++q) {
+            const int64_t kr = (wave * NBI + q) * Cfg::RPI + lane / Cfg::LPR;
+            const int64_t gc = col0 + (lane % Cfg::LPR) * 4;
+            poffB[q] = uint32_t(kr * N * 4 + (gc < N ? gc : N - 4) * 4);
+        }
+        const unsigned char* const a_row0 = reinterpret_cast<const unsigned char*>(A + row0 * K);
+        const unsigned char* const b_col0 = reinterpret_cast<const unsigned char*>(B);
+        auto pipe_loads = [&](int64_t t, int buf) __attribute__((always_inline)) {
+            T* adst = As0 + buf * (BM * BK);
+            T* bdst = Bs0 + buf * (BK * BN);
+            const unsigned char* ap = a_row0 + t * (BK * 4);
+            const unsigned char* bp = b_col0 + t * (BK * N * 4);
+#pragma unroll
+            for (int q = 0; q < NAI; ++q) lds_load16(ap + poffA[q], adst + (wave * NAI + q) * 256);
+#pragma unroll
+            for (int q = 0; q < NBI; ++q) lds_load16(bp + poffB[q], bdst + (wave * NBI + q) * 256);
+        };
+        // Fragments.  B: two register sets by pair parity, bf[s][h*2 + g] = k
+        // row h of the pair, column quad g.  A: one set, af[i] = the pair's
+        // two k of row i, refilled half a pair behind the folds.  Pair P runs
+        // as: fold rows 0-3; read rows 0-3 and B of P+1; wait for rows 4-7 of
+        // P; fold them; read rows 4-7 of P+1; wait for rows 0-3 and B of P+1
+        // (8, then 12 reads in flight; the waits count them).
+        V4 bf[2][4];
+        V2 af[TM];
+        auto read_b = [&](auto pc, uint32_t bbuf, int set) __attribute__((always_inline)) {
+            constexpr int P = decltype(pc)::value;
+            lds_read16_nowait<P * 1024>(bf[set][0], bbuf);
+            lds_read16_nowait<P * 1024 + 256>(bf[set][1], bbuf);
+            lds_read16_nowait<P * 1024 + 512>(bf[set][2], bbuf);
+            lds_read16_nowait<P * 1024 + 768>(bf[set][3], bbuf);
+        };
+        auto read_a_half = [&](auto pc, auto hc, uint32_t abuf) __attribute__((always_inline)) {
+            constexpr int P = decltype(pc)::value, H = decltype(hc)::value;
+            const uint32_t addr = (sw16 ^ uint32_t((P / 2) << 4)) + abuf;
+            static_for<4>([&](auto ic) __attribute__((always_inline)) {
+                constexpr int I = decltype(ic)::value;
+                lds_read8_nowait<H * 64 * BK * 4 + I * 128 + (P & 1) * 8>(af[H * 4 + I], addr);
+            });
+        };
+        // Folds rows [I0, I1) of the pair into acc, row by row, each row's
+        // results pinned so the fold happens here (the instruction selector
+        // would otherwise place it after later asm statements: nothing else
+        // ties it) and a row's temporaries die before the next row starts.
+        auto fold_rows = [&](auto i0c, auto i1c, int sb) __attribute__((always_inline)) {
+            constexpr int I0 = decltype(i0c)::value, I1 = decltype(i1c)::value;
+#pragma unroll
+            for (int i = I0; i < I1; ++i) {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const T p0 = tmul<SR, T>(af[i][0], bf[sb][j >> 2][j & 3]);
+                    const T p1 = tmul<SR, T>(af[i][1], bf[sb][2 + (j >> 2)][j & 3]);
+                    acc[i][j] = tjoin<SR, T>(tjoin<SR, T>(acc[i][j], p0), p1);
+                }
+                pin8(acc[i][0], acc[i][1], acc[i][2], acc[i][3], acc[i][4], acc[i][5], acc[i][6],
+                     acc[i][7]);
+            }
+        };
+        constexpr int PAIRS = BK / 2;
+        // Prologue: tile t0 in LDS (and t0 + 1 on its way), the first pair's
+        // fragments read.
+        pipe_loads(t0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // Tile count as a 32-bit scalar (the loop's control stays in SGPRs).
+        const int ntiles = __builtin_amdgcn_readfirstlane(int(t1 - t0));
+        if (ntiles > 1) pipe_loads(t0 + 1, 1);
+        read_a_half(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_thr);
+        read_b(std::integral_constant<int, 0>{}, b_thr, 0);
+        read_a_half(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, a_thr);
+        lds_wait(af[0], af[1], af[2], af[3], af[4], af[5], af[6], af[7]);
+        lds_wait(bf[0][0], bf[0][1], bf[0][2], bf[0][3]);
+        for (int it = 0; it < ntiles; ++it) {
+            const int64_t t = t0 + it;
+            const int buf = it & 1;
+            const uint32_t abuf = a_thr + uint32_t(buf) * Cfg::A_BYTES;
+            const uint32_t bbuf = b_thr + uint32_t(buf) * Cfg::B_BYTES;
+            const uint32_t abuf_n = a_thr + uint32_t(buf ^ 1) * Cfg::A_BYTES;
+            const uint32_t bbuf_n = b_thr + uint32_t(buf ^ 1) * Cfg::B_BYTES;
+            const bool more = it + 1 < ntiles;
+            static_for<PAIRS>([&](auto pc) __attribute__((always_inline)) {
+                constexpr int P = decltype(pc)::value;
+                constexpr int NP = P + 1;
+                constexpr int SB = P & 1;
+                fold_rows(std::integral_constant<int, 0>{}, std::integral_constant<int, 4>{}, SB);
+                __builtin_amdgcn_sched_barrier(0);
+                bool issued = true;
+                if constexpr (NP < PAIRS) {
+                    read_a_half(std::integral_constant<int, NP>{}, std::integral_constant<int, 0>{}, abuf);
+                    read_b(std::integral_constant<int, NP>{}, bbuf, NP & 1);
+                } else if (more) {
+                    // Tile t+1 complete in LDS, and every wave done reading
+                    // tile t (their reads were waited for): load t+2 into
+                    // this buffer, read t+1's first pair.
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    __syncthreads();
+                    if (it + 2 < ntiles) pipe_loads(t + 2, buf);
+                    read_a_half(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, abuf_n);
+                    read_b(std::integral_constant<int, 0>{}, bbuf_n, 0);
+                } else {
+                    issued = false;
+                }
+                // Rows 4-7 of pair P: their reads are older than the eight
+                // just issued.
+                if (issued)
+                    lds_wait<8>(af[4], af[5], af[6], af[7]);
+                else
+                    lds_wait<0>(af[4], af[5], af[6], af[7]);
+                __builtin_amdgcn_sched_barrier(0);
+                fold_rows(std::integral_constant<int, 4>{}, std::integral_constant<int, 8>{}, SB);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (NP < PAIRS) {
+                    read_a_half(std::integral_constant<int, NP>{}, std::integral_constant<int, 1>{}, abuf);
+                    lds_wait<4>(af[0], af[1], af[2], af[3], bf[NP & 1][0], bf[NP & 1][1],
+                                bf[NP & 1][2], bf[NP & 1][3]);
+                } else if (more) {
+                    read_a_half(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{}, abuf_n);
+                    lds_wait<4>(af[0], af[1], af[2], af[3], bf[0][0], bf[0][1], bf[0][2], bf[0][3]);
+                }
+            });
+        }
+    } else {
     if (TAILK && t1 - 1 == t0)
         issue_tail_loads(t0, 0);
     else
@@ -454,6 +674,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int s = 0; s < BK / CL; ++s) chunk(t, buf, s, acc, acc);
         }
+    }
     }
 
     // ---- epilogue ------------------------------------------------------------
@@ -611,6 +832,34 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 }
             }
         };
+        // One list entry's resolve: first k of its window attaining the
+        // window's optimum, and for a zero optimum the sign of that
+        // product; written over the entry's chunk slot.
+        auto resolve_entry = [&](int e, const Window& cur) __attribute__((always_inline)) {
+            T p[CL];
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) p[w * 4 + q] = tmul<SR, T>(cur.a[w].v[q], cur.b[w].v[q]);
+            T mx = tjoin<SR, T>(p[0], p[1]);
+#pragma unroll
+            for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
+            uint32_t bits = 0;
+#pragma unroll
+            for (int kk = 0; kk < CL; ++kk) bits |= (p[kk] == mx) ? (1u << kk) : 0u;
+            const int f = bits ? int(__builtin_ctz(bits)) : 0;
+            int r = f;
+            if constexpr (std::is_floating_point<T>::value) {
+                if (mx == T(0)) {
+                    const T* ap;
+                    const T* bp;
+                    window_ptrs(e, ap, bp);
+                    const T bf = BDIRECT ? bp[int64_t(f) * N] : bp[f];
+                    if (__builtin_signbit(tmul<SR, T>(ap[f], bf))) r |= 32;
+                }
+            }
+            chs[int(list[e])] = uint16_t(r);
+        };
         if (tid < total) {
             Window cur;
             load_window(tid, cur);
@@ -621,30 +870,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
                 const int en = e + TG_THREADS < total ? e + TG_THREADS : e;
                 Window nxt;
                 load_window(en, nxt);
-                T p[CL];
-#pragma unroll
-                for (int w = 0; w < NW; ++w)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) p[w * 4 + q] = tmul<SR, T>(cur.a[w].v[q], cur.b[w].v[q]);
-                T mx = tjoin<SR, T>(p[0], p[1]);
-#pragma unroll
-                for (int kk = 2; kk < CL; kk += 2) mx = tjoin<SR, T>(tjoin<SR, T>(mx, p[kk]), p[kk + 1]);
-                // First match: independent match bits, then the lowest.
-                uint32_t bits = 0;
-#pragma unroll
-                for (int kk = 0; kk < CL; ++kk) bits |= (p[kk] == mx) ? (1u << kk) : 0u;
-                const int f = bits ? int(__builtin_ctz(bits)) : 0;
-                int r = f;
-                if constexpr (std::is_floating_point<T>::value) {
-                    if (mx == T(0)) {
-                        const T* ap;
-                        const T* bp;
-                        window_ptrs(e, ap, bp);
-                        const T bf = BDIRECT ? bp[int64_t(f) * N] : bp[f];
-                        if (__builtin_signbit(tmul<SR, T>(ap[f], bf))) r |= 32;
-                    }
-                }
-                chs[int(list[e])] = uint16_t(r);
+                resolve_entry(e, cur);
                 cur = nxt;
             }
         }
