@@ -1,6 +1,6 @@
 """Benchmark of the tropical GEMM hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P|C1|C2|C3|C4|C5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config P|C1|...|I2|E1]
 
 A step is one call of the C ABI entry point ``tg_gemm_ws`` on the config's
 synthetic inputs (already resident in HBM): for argmax configs that is the
@@ -47,6 +47,12 @@ PEAK_FP64_TFLOPS = 78.6       # MI355X published FP64 vector peak
 # (2 tropical ops per 2 instructions) at the FP64 instruction peak (78.6
 # TFLOP/s = 39.3e12 FMA lane-instructions/s): 39.3e12 tropical ops/s.
 TROP_PEAK_F64_TOPS = PEAK_FP64_TFLOPS / 2
+# i64: one v_lshl_add_u64 (the wrapping add) and a max written as
+# v_cmp_gt_i64 + two v_cndmask_b32 per product, 4 instructions for 2
+# tropical ops.  MI355X publishes no 64-bit integer vector peak; at the
+# 64-bit (FP64) instruction rate, 39.3e12 lane-instructions/s, that is
+# 19.65e12 tropical ops/s (a register-only probe of the mix sustains 18.2e12).
+TROP_PEAK_I64_TOPS = PEAK_FP64_TFLOPS / 4
 DTYPE_NAME = {"f32": "f32", "f64": "f64", "i32": "i32", "i64": "i64"}
 WORKLOAD_NAMES = {
     "P": "P: MaxPlus f32 4096^3 +argmax (BASELINE configs[4] forward)",
@@ -58,6 +64,8 @@ WORKLOAD_NAMES = {
     "M1": "M1: MaxPlus f32 65536x2048x8 +argmax (short K, HBM-bound)",
     "F1": "F1: MaxPlus f64 4096^3 +argmax",
     "F2": "F2: MaxPlus f64 4096^3 value-only",
+    "I1": "I1: MaxPlus i64 4096^3 +argmax",
+    "I2": "I2: MaxPlus i64 4096^3 value-only",
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
@@ -69,6 +77,8 @@ KERNEL_NAMES = {
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
     "F1": "tg_gemm_dl64<MaxPlus> (f64, 64x128 tiles, argmax)",
     "F2": "tg_gemm_dl64<MaxPlus, value-only> (f64, 64x128 tiles)",
+    "I1": "tg_gemm_tiles<MaxPlus, i64, chunked argmax> (64x64 tiles)",
+    "I2": "tg_gemm_tiles<MaxPlus, i64, value-only> (64x64 tiles)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
@@ -96,7 +106,7 @@ def cpu_model() -> str:
 # about 0.5-4 s of single-core work.  C1 and C4 run whole; M1's short K makes
 # the reference's blocked loops slow (0.07 GOP/s), hence its small slab.
 CPU_ROWS = {"C1": 1024, "C2": 512, "C3": 1024, "C4": 262144, "C5": 512, "M1": 4096, "F1": 256,
-            "F2": 4096}
+            "F2": 4096, "I1": 768, "I2": 768}
 # Configurations without a CPU restatement of the reference path they would
 # take, with the reason (none at present: every configuration has one).
 NO_CPU_BASELINE: dict = {}
@@ -125,6 +135,9 @@ def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> di
                                             "microkernel)")
     elif ha.dtype == np.float32:
         fn, algo = oracle.avx2_gemm_f32, ("value-only algorithm (BLIS F32_AVX2 tiling, AVX2 8x8 "
+                                          "microkernel)")
+    elif ha.dtype in (np.int32, np.int64):
+        fn, algo = oracle.portable_gemm, ("value-only algorithm (BLIS PORTABLE tiling, 4x4 scalar "
                                           "microkernel)")
     elif ha.dtype == np.float64 and sr == "maxplus":
         fn, algo = oracle.avx2_gemm_maxplus_f64, ("value-only algorithm (BLIS F64_AVX2 tiling, AVX2 "
@@ -262,7 +275,8 @@ def main() -> int:
     # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--config", default="P",
-                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "F2", "E1"])
+                    choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "F2", "I1", "I2",
+                             "E1"])
     ap.add_argument("--cpu-rows", type=int, default=3072,
                     help="rows of P's CPU-baseline slab (0 skips the CPU baseline of every "
                          "configuration)")
@@ -387,10 +401,11 @@ def main() -> int:
     else:
         # Tropical (+)/(x) has no MFMA form: the kernel is bound by the
         # vector ALU.  peak = MI355X published vector peak of the dtype.
-        peak = PEAK_FP64_TFLOPS if cfg["dtype"] == "f64" else PEAK_FP32_TFLOPS
+        peak = PEAK_FP64_TFLOPS if cfg["dtype"] in ("f64", "i64") else PEAK_FP32_TFLOPS
         roofline = {"bound": "valu", "achieved": round(kernel_tops, 3), "peak": peak,
                     "unit": "TFLOP/s", "frac": round(kernel_tops / peak, 4)}
-    trop_peak = TROP_PEAK_F64_TOPS if cfg["dtype"] == "f64" else TROP_PEAK_TOPS
+    trop_peak = {"f64": TROP_PEAK_F64_TOPS, "i64": TROP_PEAK_I64_TOPS}.get(cfg["dtype"],
+                                                                          TROP_PEAK_TOPS)
     roofline.update({
         "traffic": TRAFFIC.get(args.config),
         "kernel": KERNEL_NAMES[args.config],

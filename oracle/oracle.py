@@ -57,9 +57,14 @@ def _load():
             fn = getattr(lib, name)
             fn.argtypes = [vp, vp, vp, vp, i64, i64, i64]
             fn.restype = None
-        for name in ("tgo_portable_argmax_f32", "tgo_portable_argmax_f64", "tgo_portable_argmax_i32"):
+        for name in ("tgo_portable_argmax_f32", "tgo_portable_argmax_f64", "tgo_portable_argmax_i32",
+                     "tgo_portable_argmax_i64"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.c_int, vp, vp, vp, vp, i64, i64, i64]
+            fn.restype = ctypes.c_int
+        for name in ("tgo_portable_gemm_i32", "tgo_portable_gemm_i64"):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.c_int, vp, vp, vp, i64, i64, i64]
             fn.restype = ctypes.c_int
         lib.tgo_avx2_gemm_f32.argtypes = [ctypes.c_int, vp, vp, vp, i64, i64, i64]
         lib.tgo_avx2_gemm_f32.restype = ctypes.c_int
@@ -140,11 +145,12 @@ def backward_b(grad_c: np.ndarray, argmax: np.ndarray, k: int, a: np.ndarray | N
 
 def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
     """Single-thread restatement of the reference CPU argmax path (BLIS
-    PORTABLE tiling + 4x4 scalar microkernel) for float32, float64 or int32
-    operands; used as the timed baseline."""
+    PORTABLE tiling + 4x4 scalar microkernel) for float32, float64, int32 or
+    int64 operands; used as the timed baseline."""
     dt = np.dtype(a.dtype)
-    if dt not in (np.dtype(np.float32), np.dtype(np.float64), np.dtype(np.int32)):
-        raise ValueError(f"portable baseline restated for float32, float64 and int32, got {dt}")
+    if dt not in (np.dtype(np.float32), np.dtype(np.float64), np.dtype(np.int32),
+                  np.dtype(np.int64)):
+        raise ValueError(f"portable baseline restated for float32, float64, int32 and int64, got {dt}")
     a = np.ascontiguousarray(a, dtype=dt)
     b = np.ascontiguousarray(b, dtype=dt)
     m, k = a.shape
@@ -153,7 +159,8 @@ def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
     am = np.empty((m, n), dtype=np.uint32)
     fn = {np.dtype(np.float32): _load().tgo_portable_argmax_f32,
           np.dtype(np.float64): _load().tgo_portable_argmax_f64,
-          np.dtype(np.int32): _load().tgo_portable_argmax_i32}[dt]
+          np.dtype(np.int32): _load().tgo_portable_argmax_i32,
+          np.dtype(np.int64): _load().tgo_portable_argmax_i64}[dt]
     rc = fn(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), _ptr(am), m, n, k)
     if rc != 0:
         raise ValueError("oracle rejected arguments")
@@ -163,6 +170,28 @@ def portable_argmax(semiring: str, a: np.ndarray, b: np.ndarray):
 def portable_argmax_f32(semiring: str, a: np.ndarray, b: np.ndarray):
     """float32 form of ``portable_argmax``."""
     return portable_argmax(semiring, np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
+
+
+def portable_gemm(semiring: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Single-thread restatement of the reference CPU value-only path for
+    integer operands (BLIS PORTABLE tiling + 4x4 value microkernel,
+    core/kernel.rs:72-117; simd/dispatch.rs:233-242 sends every i32 / i64
+    semiring there); used as the timed baseline of value-only integer
+    configurations."""
+    dt = np.dtype(a.dtype)
+    if dt not in (np.dtype(np.int32), np.dtype(np.int64)):
+        raise ValueError(f"portable value baseline restated for int32 and int64, got {dt}")
+    a = np.ascontiguousarray(a, dtype=dt)
+    b = np.ascontiguousarray(b, dtype=dt)
+    m, k = a.shape
+    n = b.shape[1]
+    c = np.empty((m, n), dtype=dt)
+    fn = {np.dtype(np.int32): _load().tgo_portable_gemm_i32,
+          np.dtype(np.int64): _load().tgo_portable_gemm_i64}[dt]
+    rc = fn(SEMIRINGS[semiring], _ptr(a), _ptr(b), _ptr(c), m, n, k)
+    if rc != 0:
+        raise ValueError("oracle rejected arguments")
+    return c
 
 
 def avx2_gemm_maxplus_f64(semiring: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -30,7 +30,7 @@
  *     pthreads.  Results are therefore identical to the reference CPU path
  *     for every non-NaN input (NaN handling also follows the select rule).
  *
- *  2. tgo_portable_argmax_{f32,f64,i32}, tgo_avx2_gemm_f32 and
+ *  2. tgo_portable_argmax_{f32,f64,i32,i64}, tgo_portable_gemm_{i32,i64}, tgo_avx2_gemm_f32 and
  *     tgo_avx2_gemm_maxplus_f64 : the CPU BASELINES used for timing.  Faithful single-thread restatements of the
  *     reference's two CPU paths:
  *       argmax (every dtype): BLIS 5-loop with TilingParams::PORTABLE
@@ -363,6 +363,78 @@ TGO_BACKWARD_B(tgo_backward_b_f64, double)
 TGO_PORTABLE(float, f32, zero_f32, mul_f32)
 TGO_PORTABLE(double, f64, zero_f64, mul_f64)
 TGO_PORTABLE(int32_t, i32, zero_i32, mul_i32)
+TGO_PORTABLE(int64_t, i64, zero_i64, mul_i64)
+
+/* ------------------------------------------------------------------------ */
+/* CPU BASELINE for value-only integer products: the reference's portable   */
+/* value path (simd/dispatch.rs:233-242 sends every i32 / i64 semiring to    */
+/* PortableKernel with TilingParams::PORTABLE): the same 5-loop driver and   */
+/* packing as above, and the 4x4 value microkernel of core/kernel.rs:72-117  */
+/* (load the accumulators from C, acc = acc (+) a (x) b for k ascending,     */
+/* store back).  (+) is max (MaxPlus, MaxMul) or min (MinPlus); on integers  */
+/* the reference's tropical_add returns the same value whichever way ties   */
+/* go (types/max_plus.rs, min_plus.rs, max_mul.rs).                          */
+/* ------------------------------------------------------------------------ */
+#define TGO_PORTABLE_VALUE(T, S, ZERO, MUL)                                                     \
+    static void micro_value_##S(int sr, int64_t mr, int64_t nr, int64_t kc, const T* pa,       \
+                                const T* pb, T* c, int64_t ldc) {                               \
+        T acc[P_MR][P_NR];                                                                      \
+        for (int64_t i = 0; i < P_MR; ++i)                                                      \
+            for (int64_t j = 0; j < P_NR; ++j) acc[i][j] = ZERO(sr);                            \
+        for (int64_t i = 0; i < mr; ++i)                                                        \
+            for (int64_t j = 0; j < nr; ++j) acc[i][j] = c[i * ldc + j];                        \
+        for (int64_t p = 0; p < kc; ++p)                                                        \
+            for (int64_t i = 0; i < mr; ++i) {                                                  \
+                const T av = pa[p * P_MR + i];                                                  \
+                for (int64_t j = 0; j < nr; ++j) {                                              \
+                    const T prod = MUL(sr, av, pb[p * P_NR + j]);                               \
+                    if (sr == TGO_MINPLUS ? prod < acc[i][j] : prod > acc[i][j]) acc[i][j] = prod; \
+                }                                                                               \
+            }                                                                                   \
+        for (int64_t i = 0; i < mr; ++i)                                                        \
+            for (int64_t j = 0; j < nr; ++j) c[i * ldc + j] = acc[i][j];                        \
+    }                                                                                           \
+    int tgo_portable_gemm_##S(int sr, const T* A, const T* B, T* C, int64_t M, int64_t N,     \
+                              int64_t K) {                                                      \
+        if (sr < 0 || sr > 2 || M < 0 || N < 0 || K < 0) return -1;                             \
+        for (int64_t t = 0; t < M * N; ++t) C[t] = ZERO(sr);                                    \
+        if (M == 0 || N == 0 || K == 0) return 0;                                               \
+        T* pa = (T*)malloc(sizeof(T) * P_MC * P_KC);                                            \
+        T* pb = (T*)malloc(sizeof(T) * P_KC * P_NC);                                            \
+        if (!pa || !pb) {                                                                       \
+            free(pa);                                                                           \
+            free(pb);                                                                           \
+            return -2;                                                                          \
+        }                                                                                       \
+        for (int64_t jc = 0; jc < N; jc += P_NC) {                                              \
+            const int64_t nc = N - jc < P_NC ? N - jc : P_NC;                                   \
+            for (int64_t pc = 0; pc < K; pc += P_KC) {                                          \
+                const int64_t kc = K - pc < P_KC ? K - pc : P_KC;                               \
+                pack_b_##S(kc, nc, B + pc * N + jc, N, pb);                                     \
+                for (int64_t ic = 0; ic < M; ic += P_MC) {                                      \
+                    const int64_t mc = M - ic < P_MC ? M - ic : P_MC;                           \
+                    pack_a_##S(mc, kc, A + ic * K + pc, K, pa);                                 \
+                    for (int64_t jr = 0; jr * P_NR < nc; ++jr) {                                \
+                        const int64_t j0 = jr * P_NR;                                           \
+                        const int64_t nr = nc - j0 < P_NR ? nc - j0 : P_NR;                     \
+                        for (int64_t ir = 0; ir * P_MR < mc; ++ir) {                            \
+                            const int64_t i0 = ir * P_MR;                                       \
+                            const int64_t mr = mc - i0 < P_MR ? mc - i0 : P_MR;                 \
+                            micro_value_##S(sr, mr, nr, kc, pa + ir * P_MR * kc,                \
+                                            pb + jr * P_NR * kc, C + (ic + i0) * N + (jc + j0), \
+                                            N);                                                 \
+                        }                                                                       \
+                    }                                                                           \
+                }                                                                               \
+            }                                                                                   \
+        }                                                                                       \
+        free(pa);                                                                               \
+        free(pb);                                                                               \
+        return 0;                                                                               \
+    }
+
+TGO_PORTABLE_VALUE(int32_t, i32, zero_i32, mul_i32)
+TGO_PORTABLE_VALUE(int64_t, i64, zero_i64, mul_i64)
 
 /* ------------------------------------------------------------------------ */
 /* CPU BASELINE for value-only f32: the reference's AVX2 path                */

@@ -130,3 +130,29 @@ def test_f64_configs_full_size(name, with_argmax, plan):
     np.testing.assert_array_equal(tc.bits(c.cpu().numpy()[rows]), tc.bits(c_ref))
     if with_argmax:
         np.testing.assert_array_equal(am.cpu().numpy()[rows], am_ref.astype(np.int32))
+
+
+@pytest.mark.parametrize("name,with_argmax,plan", [("I1", True, "tiles_chunked"),
+                                                   ("I2", False, "tiles")])
+def test_i64_configs_full_size(name, with_argmax, plan):
+    """I1 / I2 (MaxPlus i64 4096^3, entries in [-10^9, 10^9]) at full size:
+    argmax consistency on every output (I1), the oracle on sampled rows
+    (values and argmax bit-exact), and the value-only run equal to the
+    argmax run's values on every output."""
+    from tropical_gemm import _native as nat
+
+    assert nat.gemm_plan("maxplus", "i64", 4096, 4096, 4096, with_argmax) == plan
+    cfg, a, b, c, am = _run(name, with_argmax)
+    if with_argmax:
+        _check_consistency(cfg["semiring"], a, b, c, am)
+    rows = np.array([0, 1, 2, 63, 64, 1000, 2047, 4095])
+    c_ref, am_ref = oracle.gemm(cfg["semiring"], a[rows].cpu().numpy(), b.cpu().numpy())
+    np.testing.assert_array_equal(c.cpu().numpy()[rows], c_ref)
+    if with_argmax:
+        np.testing.assert_array_equal(am.cpu().numpy()[rows], am_ref.astype(np.int32))
+    else:
+        from tropical_gemm import ops
+
+        c2, am2 = ops.gemm(cfg["semiring"], a, b, True)
+        assert torch.equal(c, c2)
+        _check_consistency(cfg["semiring"], a, b, c, am2)

@@ -210,6 +210,36 @@ def test_portable_baseline_i32_equals_oracle(sr):
 
 
 @pytest.mark.parametrize("sr", tc.SEMIRINGS)
+def test_portable_baselines_i64_equal_oracle(sr):
+    # The i64 argmax and value-only restatements: K = 300 crosses the 256-k
+    # block, 67 x 130 leaves partial 4 x 4 micro-blocks; ties, and wrapping
+    # sums and products near the int64 limits.  The value path is also
+    # pinned by numpy brute force on a corner (wrapping adds and products).
+    rng = np.random.default_rng(15)
+    for lo, hi in ((-10**12, 10**12), (0, 3), (2**63 - 60, 2**63 - 1)):
+        a = rng.integers(lo, hi, size=(67, 300), dtype=np.int64)
+        b = rng.integers(-5, 60, size=(300, 130)).astype(np.int64)
+        c1, a1 = oracle.gemm(sr, a, b)
+        c2, a2 = oracle.portable_argmax(sr, a, b)
+        np.testing.assert_array_equal(c1, c2)
+        np.testing.assert_array_equal(a1, a2)
+        c3 = oracle.portable_gemm(sr, a, b)
+        np.testing.assert_array_equal(c1, c3)
+        with np.errstate(over="ignore"):
+            prod = (a[:5, :, None] * b[None, :, :7]) if sr == "maxmul" else (a[:5, :, None] + b[None, :, :7])
+        ref = prod.min(axis=1) if sr == "minplus" else prod.max(axis=1)
+        np.testing.assert_array_equal(c3[:5, :7], ref)
+    # int32 value path against the oracle; empty K gives the tropical zero.
+    a = rng.integers(-1000, 1001, size=(67, 300)).astype(np.int32)
+    b = rng.integers(-1000, 1001, size=(300, 130)).astype(np.int32)
+    np.testing.assert_array_equal(oracle.portable_gemm(sr, a, b),
+                                  oracle.gemm(sr, a, b, with_argmax=False)[0])
+    z = oracle.portable_gemm(sr, np.zeros((3, 0), np.int64), np.zeros((0, 5), np.int64))
+    zero = {"maxplus": np.iinfo(np.int64).min, "minplus": np.iinfo(np.int64).max, "maxmul": 0}[sr]
+    np.testing.assert_array_equal(z, np.full((3, 5), zero, np.int64))
+
+
+@pytest.mark.parametrize("sr", tc.SEMIRINGS)
 def test_avx2_value_baseline_equals_oracle(sr):
     # 300 x 600 x 270 crosses every block edge of the 256/256/512 tiling and
     # leaves partial 8 x 8 micro-blocks; MaxMul on positive data.

@@ -14,6 +14,8 @@ the host) to the CPU oracle.  Nothing here reads the reference.
         HBM (the 0.5 GB output and argmax writes), not by the VALU
     F1  MaxPlus f64 4096^3 with argmax, A, B ~ N(0,1) (the f64 kernels)
     F2  MaxPlus f64 4096^3 value-only, A, B ~ N(0,1)
+    I1  MaxPlus i64 4096^3 with argmax, A, B uniform integers in [-10^9, 10^9]
+    I2  MaxPlus i64 4096^3 value-only, same inputs
     E1  tropical einsum "jik,lkj,lm->im", MaxPlus f32, N(0,1): i = l = m = 2048,
         j = 32, k = 64 (two 2048^3 contractions after two permutations)
 """
@@ -34,6 +36,8 @@ CONFIGS = {
     "M1": dict(semiring="maxplus", dtype="f32", m=65536, k=8, n=2048, argmax=True, bound="hbm"),
     "F1": dict(semiring="maxplus", dtype="f64", m=4096, k=4096, n=4096, argmax=True),
     "F2": dict(semiring="maxplus", dtype="f64", m=4096, k=4096, n=4096, argmax=False),
+    "I1": dict(semiring="maxplus", dtype="i64", m=4096, k=4096, n=4096, argmax=True),
+    "I2": dict(semiring="maxplus", dtype="i64", m=4096, k=4096, n=4096, argmax=False),
 }
 
 
@@ -66,6 +70,12 @@ def make_inputs(name: str, device="cuda", scale: float = 1.0):
                           dtype=torch.int32)
         b = torch.randint(-50, 1, (k, n), generator=_gen(device, idx, 1), device=device,
                           dtype=torch.int32)
+    elif name in ("I1", "I2"):
+        lim = 10**9
+        a = torch.randint(-lim, lim + 1, (m, k), generator=_gen(device, idx, 0), device=device,
+                          dtype=torch.int64)
+        b = torch.randint(-lim, lim + 1, (k, n), generator=_gen(device, idx, 1), device=device,
+                          dtype=torch.int64)
     else:
         raise KeyError(name)
     return a.contiguous(), b.contiguous()
