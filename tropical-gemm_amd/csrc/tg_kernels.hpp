@@ -390,24 +390,12 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         else
             cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
     };
-    if constexpr (!ARGMAX || EXACT) {
-        if constexpr (!EXACT) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
-                    const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
-                    if ((danger || tisnan(acc[i][j])) && gr < M && gc < N) {
-                        int32_t ix;
-                        exact(gr, gc, acc[i][j], ix);
-                    }
-                }
-        }
-        // Values (and EXACT indices) as they stand.  Each thread's columns
-        // come in groups of 4 consecutive ones: one 16-byte store per group
-        // and array when the rows are 16-byte aligned, element stores at the
-        // ragged right edge or otherwise.
+    // Values and indices as they stand in acc / ch (the chunked argmax writes
+    // its resolved outputs back there first).  Each thread's columns come in
+    // groups of 4 consecutive ones: one 16-byte store per group and array
+    // when the rows are 16-byte aligned, element stores at the ragged right
+    // edge or otherwise.
+    auto store_outputs = [&]() {
         const bool vec_out = N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
                              (!ARGMAX || (reinterpret_cast<uintptr_t>(IDX) & 15u) == 0);
 #pragma unroll
@@ -456,6 +444,22 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                 }
             }
         }
+    };
+    if constexpr (!ARGMAX || EXACT) {
+        if constexpr (!EXACT) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+                    const int64_t gc = col0 + (j / 4) * 64 + tx * 4 + (j % 4);
+                    if ((danger || tisnan(acc[i][j])) && gr < M && gc < N) {
+                        int32_t ix;
+                        exact(gr, gc, acc[i][j], ix);
+                    }
+                }
+        }
+        store_outputs();
     } else {
         // Exact argmax inside the recorded chunk.  Products in the chunk
         // before it never equal the final value (that chunk would not have
@@ -548,14 +552,14 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                         val[g] = tzero<SR, T>();
                         idx[g] = 0;
                     }
-                    if (gr < M && gc[g] < N) {
-                        if (danger || tisnan(acc[i][j0 + g])) exact(gr, gc[g], val[g], idx[g]);
-                        C[gr * N + gc[g]] = val[g];
-                        IDX[gr * N + gc[g]] = idx[g];
-                    }
+                    if (gr < M && gc[g] < N && (danger || tisnan(acc[i][j0 + g])))
+                        exact(gr, gc[g], val[g], idx[g]);
+                    acc[i][j0 + g] = val[g];
+                    ch[i][j0 + g] = idx[g];
                 }
             }
         }
+        store_outputs();
     }
 }
 
