@@ -390,56 +390,54 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
         else
             cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
     };
-    // Values and indices as they stand in acc / ch (the chunked argmax writes
-    // its resolved outputs back there first).  Each thread's columns come in
+    // Row i of the thread's values and indices as they stand in acc / ch (the
+    // chunked argmax writes a row's resolved outputs back there first, so the
+    // row's registers are free after its stores).  Each thread's columns come in
     // groups of 4 consecutive ones: one 16-byte store per group and array
     // when the rows are 16-byte aligned, element stores at the ragged right
     // edge or otherwise.
-    auto store_outputs = [&]() {
-        const bool vec_out = N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
-                             (!ARGMAX || (reinterpret_cast<uintptr_t>(IDX) & 15u) == 0);
+    const bool vec_out = N % 4 == 0 && (reinterpret_cast<uintptr_t>(C) & 15u) == 0 &&
+                         (!ARGMAX || (reinterpret_cast<uintptr_t>(IDX) & 15u) == 0);
+    auto store_row = [&](const int i) {
+        const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
+        if (gr >= M) return;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
-            if (gr >= M) continue;
+        for (int g = 0; g < TN / 4; ++g) {
+            const int64_t gc = col0 + g * 64 + tx * 4;
+            if (vec_out && gc + 3 < N) {
+                T cv[4];
+                int32_t iv[4];
 #pragma unroll
-            for (int g = 0; g < TN / 4; ++g) {
-                const int64_t gc = col0 + g * 64 + tx * 4;
-                if (vec_out && gc + 3 < N) {
-                    T cv[4];
-                    int32_t iv[4];
+                for (int e = 0; e < 4; ++e) {
+                    cv[e] = acc[i][g * 4 + e];
+                    iv[e] = ch[i][g * 4 + e];
+                }
+                static_assert(sizeof(cv) % 16 == 0, "4 values make whole 16-byte vectors");
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        cv[e] = acc[i][g * 4 + e];
-                        iv[e] = ch[i][g * 4 + e];
+                for (int w = 0; w < int(sizeof(cv)) / 16; ++w) {
+                    if constexpr (!ARGMAX) {
+                        // Value-only: non-temporal (streaming) stores,
+                        // 8-15% faster at short K on MI355X; with argmax
+                        // they were 10-20% slower, so plain stores there.
+                        typedef int v4i_t __attribute__((ext_vector_type(4)));
+                        v4i_t x;
+                        __builtin_memcpy(&x, reinterpret_cast<const char*>(cv) + 16 * w, 16);
+                        __builtin_nontemporal_store(
+                            x, reinterpret_cast<v4i_t*>(C + gr * N + gc) + w);
+                    } else {
+                        reinterpret_cast<Vec16<T>*>(C + gr * N + gc)[w] =
+                            reinterpret_cast<const Vec16<T>*>(cv)[w];
                     }
-                    static_assert(sizeof(cv) % 16 == 0, "4 values make whole 16-byte vectors");
+                }
+                if constexpr (ARGMAX)
+                    *reinterpret_cast<Vec16<int32_t>*>(IDX + gr * N + gc) =
+                        *reinterpret_cast<const Vec16<int32_t>*>(iv);
+            } else {
 #pragma unroll
-                    for (int w = 0; w < int(sizeof(cv)) / 16; ++w) {
-                        if constexpr (!ARGMAX) {
-                            // Value-only: non-temporal (streaming) stores,
-                            // 8-15% faster at short K on MI355X; with argmax
-                            // they were 10-20% slower, so plain stores there.
-                            typedef int v4i_t __attribute__((ext_vector_type(4)));
-                            v4i_t x;
-                            __builtin_memcpy(&x, reinterpret_cast<const char*>(cv) + 16 * w, 16);
-                            __builtin_nontemporal_store(
-                                x, reinterpret_cast<v4i_t*>(C + gr * N + gc) + w);
-                        } else {
-                            reinterpret_cast<Vec16<T>*>(C + gr * N + gc)[w] =
-                                reinterpret_cast<const Vec16<T>*>(cv)[w];
-                        }
-                    }
-                    if constexpr (ARGMAX)
-                        *reinterpret_cast<Vec16<int32_t>*>(IDX + gr * N + gc) =
-                            *reinterpret_cast<const Vec16<int32_t>*>(iv);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (gc + e < N) {
-                            C[gr * N + gc + e] = acc[i][g * 4 + e];
-                            if constexpr (ARGMAX) IDX[gr * N + gc + e] = ch[i][g * 4 + e];
-                        }
+                for (int e = 0; e < 4; ++e) {
+                    if (gc + e < N) {
+                        C[gr * N + gc + e] = acc[i][g * 4 + e];
+                        if constexpr (ARGMAX) IDX[gr * N + gc + e] = ch[i][g * 4 + e];
                     }
                 }
             }
@@ -459,7 +457,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                     }
                 }
         }
-        store_outputs();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) store_row(i);
     } else {
         // Exact argmax inside the recorded chunk.  Products in the chunk
         // before it never equal the final value (that chunk would not have
@@ -558,8 +557,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                     ch[i][j0 + g] = idx[g];
                 }
             }
+            store_row(i);
         }
-        store_outputs();
     }
 }
 
