@@ -84,11 +84,13 @@ KERNEL_NAMES = {
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md,
 # profiles/tg_gemm_shortk_*.md, profiles/hbm_traffic_c2_c3_e1.md,
-# profiles/tg_gemm_dl_split_*.md, profiles/tg_gemm_dl64_*.md).  E1: per GEMM
-# launch; C1: the split GEMM launch (the merge adds 0.025e9).
+# profiles/tg_gemm_dl_split_*.md, profiles/tg_gemm_dl64_*.md,
+# profiles/tg_gemm_tiles_maxplus_i64_4096.md).  E1: per GEMM launch; C1: the
+# split GEMM launch (the merge adds 0.025e9).
 
 TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.042e9,
-           "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9}
+           "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9,
+           "I1": 7.997e9, "I2": 3.356e9}
 
 
 def cpu_model() -> str:
