@@ -72,7 +72,7 @@ KERNEL_NAMES = {
     "C1": "tg_gemm_dl<MaxPlus, f32, argmax> split-K x2 + tg_merge_splits",
     "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
-    "C4": "tg_gemm_kres8<MaxPlus, K=128> (64x128 tiles, f32 keys)",
+    "C4": "tg_gemm_kresw<MaxPlus, K=128> (wave-private 16x128 tiles, f32 keys)",
     "C5": "tg_gemm_dl<MaxPlus, f32, argmax>",
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
     "F1": "tg_gemm_dl64<MaxPlus> (f64, 64x128 tiles, argmax)",
@@ -82,13 +82,13 @@ KERNEL_NAMES = {
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
 # and WRITE_SIZE, scaled by the same counters on a copy kernel of known size
-# (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kres_*.md,
+# (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kresw_*.md,
 # profiles/tg_gemm_shortk_*.md, profiles/hbm_traffic_c2_c3_e1.md,
 # profiles/tg_gemm_dl_split_*.md, profiles/tg_gemm_dl64_*.md,
 # profiles/tg_gemm_tiles_maxplus_i64_4096.md).  E1: per GEMM launch; C1: the
 # split GEMM launch (the merge adds 0.025e9).
 
-TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.403e9, "M1": 1.108e9, "C1": 0.042e9,
+TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.418e9, "M1": 1.108e9, "C1": 0.042e9,
            "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9,
            "I1": 7.997e9, "I2": 3.356e9}
 
@@ -160,6 +160,32 @@ def run_cpu_baseline(cfg: dict, a, b, rows: int, value_only: bool = False) -> di
     }
 
 
+# Untimed warm-up.  With --warmup W given: exactly W steps.  By default:
+# DEFAULT_WARMUP steps, repeated until at least WARMUP_MIN_S has passed, so
+# that short steps (C4, M1: ~0.15 ms) also run on the settled engine clock
+# (it ramps over the first ~15 ms of sustained load).  Returns the steps run.
+DEFAULT_WARMUP = 25
+WARMUP_MIN_S = 0.2
+
+
+def warm_up(step, steps, dev) -> int:
+    import torch
+
+    if steps is not None:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize(dev)
+        return steps
+    t0 = time.perf_counter()
+    done = 0
+    while done == 0 or time.perf_counter() - t0 < WARMUP_MIN_S:
+        for _ in range(DEFAULT_WARMUP):
+            step()
+        done += DEFAULT_WARMUP
+        torch.cuda.synchronize(dev)
+    return done
+
+
 def cpu_rows_for(name: str, p_rows: int) -> int:
     """P uses --cpu-rows; the others their CPU_ROWS sample."""
     return p_rows if name == "P" else CPU_ROWS[name]
@@ -203,9 +229,7 @@ def run_einsum(args, lib, dev) -> int:
     def step():
         return E.einsum(code, *ops_, semiring=sr)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize(dev)
+    warmup_run = warm_up(step, args.warmup, dev)
     stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -236,7 +260,7 @@ def run_einsum(args, lib, dev) -> int:
         "unit": "GOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup_run,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -274,8 +298,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     # The engine clock ramps from ~2.1 to ~2.35 GHz over the first ~15 ms of
-    # sustained VALU load; 25 warmup steps (~60 ms at P) time the settled clock.
-    ap.add_argument("--warmup", type=int, default=25)
+    # sustained VALU load.  Default: 25-step rounds until 0.2 s have passed.
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--config", default="P",
                     choices=["P", "C1", "C2", "C3", "C4", "C5", "M1", "F1", "F2", "I1", "I2",
                              "E1"])
@@ -338,9 +362,7 @@ def main() -> int:
         if backward:
             backward_only()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize(dev)
+    warmup_run = warm_up(step, args.warmup, dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     # Step timing: events on the stream every kernel of the step runs on.
@@ -424,7 +446,7 @@ def main() -> int:
         "unit": "GOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup_run,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

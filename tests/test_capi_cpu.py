@@ -125,7 +125,7 @@ def test_python_layer_rejects_host_tensors():
     ("maxplus", "f32", 4096, 4096, 4096, True, "dl_4x8_cl16"),       # P
     ("minplus", "f32", 4096, 4096, 4096, True, "dl_4x8_cl16"),       # C2
     ("maxmul", "f32", 8192, 4096, 2048, False, "dl_8x8_cl32"),       # C3
-    ("maxplus", "i32", 262144, 128, 128, True, "kres8"),             # C4
+    ("maxplus", "i32", 262144, 128, 128, True, "kresw"),             # C4
     ("maxplus", "f32", 1024, 1024, 1024, True, "dl_4x4_cl8 split 2"),  # C1
     ("maxplus", "f32", 65536, 8, 2048, True, "shortk"),              # M1 (m, k, n order below)
     ("maxplus", "f32", 67, 45, 40, True, "tiles_exact"),

@@ -731,6 +731,59 @@ def test_k_resident_several_tiles_per_workgroup(sr):
         assert_exact(c, am, *oracle.gemm(sr, x, y))
 
 
+# The wave-private K-resident kernel (tg_gemm_kresw: M a multiple of 16, N a
+# multiple of 128 up to 16 column tiles): row counts that are not multiples
+# of 64, several column tiles, fewer row tiles than waves, a wave tile that
+# leaves the key range in its last k-tile (the exact fallback after three
+# k-tiles on keys), a batch item whose B panel leaves it, and the tile after
+# a fallback back on keys.
+@pytest.mark.parametrize("sr", ["maxplus", "minplus"])
+def test_k_resident_wave_tiles(sr):
+    nat = _nat()
+    rng = np.random.default_rng(61 + (sr == "minplus"))
+    for (m, k, n, batch) in [(16, 64, 128, 1), (48, 96, 256, 2), (4112, 128, 384, 3),
+                             (2064, 128, 2048, 1)]:
+        assert nat.gemm_plan(sr, "i32", m, n, k, True) == "kresw"
+        print(f"[case] k-resident wave tiles {sr} m={m} k={k} n={n} batch={batch}", flush=True)
+        items = []
+        for t in range(batch):
+            a = rng.integers(-1000, 1001, size=(m, k))
+            b = rng.integers(-50, 1, size=(k, n))
+            a[min(m - 1, 17 + t), k - 1] = 40000  # a wave tile's last k-tile leaves the key range
+            if t == 1:
+                b[k - 1, n - 1] = -(1 << 20)  # this item's whole B panel does
+            items.append((a.astype(np.int32), b.astype(np.int32)))
+        if batch == 1:
+            a, b = items[0]
+            for api in ("alloc", "min"):
+                assert_exact(*gpu_gemm(sr, a, b, True, api=api), *oracle.gemm(sr, a, b))
+        else:
+            for (c, am), (a, b) in zip(_strided_batched(sr, items), items):
+                assert_exact(c, am, *oracle.gemm(sr, a, b))
+    # Wider than 16 column tiles: the 64 x 128 kernel (tg_gemm_kres8) keeps
+    # these, with its key path and its chunked fallback.
+    m, k, n = 192, 96, 128 * 17
+    assert nat.gemm_plan(sr, "i32", m, n, k, True) == "kres8"
+    a = rng.integers(-1000, 1001, size=(m, k))
+    b = rng.integers(-50, 1, size=(k, n))
+    a[70, 5] = 40000
+    a, b = a.astype(np.int32), b.astype(np.int32)
+    print(f"[case] k-resident 64x128 {sr} m={m} k={k} n={n}", flush=True)
+    assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+    # Ties at the f32-key boundary and wraparound through the exact path.
+    m, k, n = 272, 128, 256
+    for name, a, b in (
+        ("key boundary ties", rng.choice([-32767, 0, 32767], size=(m, k)),
+         rng.choice([-32767, 0, 32767], size=(k, n))),
+        ("wraparound", rng.integers(2**31 - 60, 2**31 - 1, size=(m, k)),
+         rng.integers(-5, 60, size=(k, n))),
+    ):
+        print(f"[case] k-resident wave tiles {sr} {name}", flush=True)
+        a = a.astype(np.int32)
+        b = b.astype(np.int32)
+        assert_exact(*gpu_gemm(sr, a, b, True), *oracle.gemm(sr, a, b))
+
+
 # Short-K i32 argmax over ragged and full-tile shapes (K in {32, 64, 96,
 # 128}, N a multiple of 64, M anything): the key-range boundary, ties,
 # wraparound, one row or one B entry just outside the f32-key range, and rows

@@ -20,6 +20,7 @@
 #include "tg_gemm_dl64.hpp"
 #include "tg_gemm_kres.hpp"
 #include "tg_gemm_kres8.hpp"
+#include "tg_gemm_kresw.hpp"
 #include "tg_gemm_shortk.hpp"
 #include "tg_kernels.hpp"
 
@@ -534,6 +535,46 @@ int run_gemm_kres8(const Problem& p, hipStream_t st) {
     return TG_OK;
 }
 
+// K-resident argmax kernel with wave-private 16-row tiles (i32
+// MaxPlus/MinPlus, N a multiple of 128): one 1024-thread workgroup per CU,
+// the CUs split evenly over the column tiles.
+template <int SR, int KT>
+int launch_kresw(const Problem& p, int64_t tiles_n, hipStream_t st) {
+    constexpr size_t lds = tg::kresw_lds_bytes(KT);
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&tg::tg_gemm_kresw<SR, KT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    TG_HIP(attr);
+    int64_t grid = (int64_t(current_cu_count()) / tiles_n) * tiles_n;
+    if (grid < tiles_n) grid = tiles_n;
+    // Fewer workgroups when the row tiles would not give each of a column
+    // tile's workgroups one tile per wave.
+    const int64_t per_col = (p.M / tg::KreswCfg::ROWS + tg::KreswCfg::WAVES - 1) / tg::KreswCfg::WAVES;
+    if (grid > per_col * tiles_n) grid = per_col * tiles_n;
+    hipLaunchKernelGGL((tg::tg_gemm_kresw<SR, KT>), dim3(unsigned(grid)), dim3(1024), lds, st,
+                       static_cast<const int32_t*>(p.A), static_cast<const int32_t*>(p.B),
+                       static_cast<int32_t*>(p.C), p.IDX, p.M, p.N, p.sA, p.sB, p.sC,
+                       int(tiles_n), p.batch);
+    return TG_OK;
+}
+
+template <int SR>
+int run_gemm_kresw(const Problem& p, hipStream_t st) {
+    using Cfg = tg::KreswCfg;
+    const int64_t tiles_n = p.N / Cfg::BN;
+    KernelTimer timer(st);
+    int rc = TG_OK;
+    switch (p.K / Cfg::BK) {
+        case 2: rc = launch_kresw<SR, 2>(p, tiles_n, st); break;
+        case 3: rc = launch_kresw<SR, 3>(p, tiles_n, st); break;
+        case 4: rc = launch_kresw<SR, 4>(p, tiles_n, st); break;
+        default: return fail(TG_ERR_INVALID_ARGUMENT, "K-resident kernel: unsupported K");
+    }
+    if (rc != TG_OK) return rc;
+    TG_HIP(hipGetLastError());
+    return TG_OK;
+}
+
 // Short-K kernel: 32 x 256 (64-bit types: 16 x 256) tiles written as 1 KB
 // row runs.
 template <int SR, typename T>
@@ -614,7 +655,7 @@ constexpr int64_t kShortkArgmaxMaxK = 32;
 constexpr int64_t kShortkValueMaxK = 63;
 
 // The kernel a problem runs on.
-enum class Path { SHORTK, KRES8, KRES, DL_88_32, DL_48_16, DL_48_VALUE, DL_44_8, DL_44_16, DL_44_32, DL64, DL64_VALUE, TILES_EXACT, TILES_CHUNKED, TILES };
+enum class Path { SHORTK, KRESW, KRES8, KRES, DL_88_32, DL_48_16, DL_48_VALUE, DL_44_8, DL_44_16, DL_44_32, DL64, DL64_VALUE, TILES_EXACT, TILES_CHUNKED, TILES };
 
 struct Plan {
     Path path = Path::TILES;
@@ -626,6 +667,7 @@ struct Plan {
 bool uses_workspace(const Plan& pl, bool argmax) {
     switch (pl.path) {
         case Path::SHORTK:
+        case Path::KRESW:
         case Path::KRES8:
         case Path::KRES:
         case Path::TILES_EXACT:
@@ -651,6 +693,10 @@ Plan plan_typed(const Problem& p, size_t ws_bytes) {
     }
     if constexpr (sizeof(T) == 4) {
         if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL) {
+            if (argmax && tg::kresw_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
+                pl.path = Path::KRESW;
+                return pl;
+            }
             if (argmax && tg::kres8_fits(p.M, p.N, p.K, p.sA, p.sB, p.sC, p.A, p.B, p.C, p.IDX)) {
                 pl.path = Path::KRES8;
                 return pl;
@@ -778,6 +824,10 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
     }
     if constexpr (sizeof(T) == 4) {
         switch (pl.path) {
+            case Path::KRESW:
+                if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL)
+                    return run_gemm_kresw<SR>(p, st);
+                break;
             case Path::KRES8:
                 if constexpr (std::is_same<T, int32_t>::value && SR != tg::SR_MAXMUL)
                     return run_gemm_kres8<SR>(p, st);
@@ -893,6 +943,7 @@ Plan plan_gemm(tg_semiring sr, tg_dtype dt, const Problem& p, size_t ws_bytes) {
 const char* path_name(Path path) {
     switch (path) {
         case Path::SHORTK: return "shortk";
+        case Path::KRESW: return "kresw";
         case Path::KRES8: return "kres8";
         case Path::KRES: return "kres";
         case Path::DL_88_32: return "dl_8x8_cl32";
