@@ -356,6 +356,36 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
             TG_HIP(attr_pipe);
         }
     }
+    // Argmax with two K slices on 64 x 64 tiles: one 512-thread workgroup per
+    // tile, each 256-thread half running one slice, merged in LDS (no
+    // partials, no merge launch).
+    constexpr bool kHalves = TM == 4 && TN == 4 && (Cfg::BK / CL) % 2 == 0;
+    if (kHalves && argmax && splits == 2 && p.K % (2 * Cfg::BK) == 0) {
+        if constexpr (kHalves) {
+            KernelTimer timer(st);
+            for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
+                const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
+                const T* Az = A + z0 * p.sA;
+                const T* Bz = B + z0 * p.sB;
+                T* Cz = C + z0 * p.sC;
+                int32_t* Iz = p.IDX + z0 * p.sC;
+                const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
+                dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
+                if (bdirect)
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, true, 0, 2>),
+                                       grid, dim3(512), 2 * Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz,
+                                       Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                                       int(tiles_n), KS, int64_t(0));
+                else
+                    hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, false, 0, 2>),
+                                       grid, dim3(512), 2 * Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz,
+                                       p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n),
+                                       KS, int64_t(0));
+                TG_HIP(hipGetLastError());
+            }
+        }
+        return TG_OK;
+    }
     KernelTimer timer(st);
     for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
         const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;

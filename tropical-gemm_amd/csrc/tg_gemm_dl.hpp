@@ -57,11 +57,14 @@ struct DlCfg {
     static constexpr int LDS_BYTES = (MISC_OFF + 64 > TILE_BYTES) ? MISC_OFF + 64 : TILE_BYTES;
 };
 
-// Exclusive prefix sum over the 256 threads of a workgroup; returns the
-// exclusive prefix of x and sets total.  scratch: 5 ints of LDS.
-__device__ __forceinline__ int block_exclusive_scan(int x, int* scratch, int& total) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+// Exclusive prefix sum over 256 threads (tid 0..255: the workgroup, or one
+// 256-thread half of it, each half with its own scratch); returns the
+// exclusive prefix of x and sets total.  scratch: 5 ints of LDS.  Every
+// thread of the workgroup calls it (it holds two barriers).
+__device__ __forceinline__ int block_exclusive_scan(int x, int* scratch, int& total,
+                                                    int tid = int(threadIdx.x)) {
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     int inc = x;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -301,8 +304,8 @@ __device__ __forceinline__ void record4(int32_t& c0, int32_t& c1, int32_t& c2, i
 // waited for explicitly), so a wave does not stall on LDS between pairs
 // (MaxPlus f32 4096^3 on MI355X: 1.847 against 1.891 ms).
 template <int SR, typename T, bool ARGMAX, int TM_, int TN_, int CL, bool TAILK = false,
-          bool BDIRECT = false, int PIPE = 0>
-__global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
+          bool BDIRECT = false, int PIPE = 0, int HALVES = 1>
+__global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_per_eu(
     PIPE != 0 ? PIPE : ARGMAX ? DlCfg<TM_, TN_>::WAVES_ARGMAX : DlCfg<TM_, TN_>::WAVES_VALUE))) void tg_gemm_dl(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
@@ -314,11 +317,19 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     static_assert(CL == 8 || CL == 16 || CL == 32, "argmax chunk of 8, 16 or 32 k");
     static_assert(!ARGMAX || (BK / CL) % 2 == 0, "argmax: an even number of chunks per k-tile");
     static_assert(!ARGMAX || TM == 4, "argmax tiles have 4 rows per thread");
-    extern __shared__ __align__(16) unsigned char dl_lds[];
+    static_assert(HALVES == 1 || (HALVES == 2 && ARGMAX && !TAILK && PIPE == 0),
+                  "two K slices per workgroup: argmax, whole k-tiles");
+    extern __shared__ __align__(16) unsigned char dl_lds_all[];
+    // HALVES == 2: the workgroup is two 256-thread halves, each running the
+    // whole kernel on its own K slice with its own LDS block; they meet
+    // only at the barriers (every barrier is reached by both) and in the
+    // merge at the end.
+    const int half = HALVES > 1 ? int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 8)) : 0;
+    unsigned char* const dl_lds = dl_lds_all + (HALVES > 1 ? half * Cfg::LDS_BYTES : 0);
     T* const As0 = reinterpret_cast<T*>(dl_lds);
     T* const Bs0 = reinterpret_cast<T*>(dl_lds + 2 * Cfg::A_BYTES);
 
-    const int tid = threadIdx.x;
+    const int tid = int(threadIdx.x) & (TG_THREADS - 1);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tx = tid & 15;
@@ -332,11 +343,13 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     B += z * sB;
     // Split K: slice y covers k in [y*KS, (y+1)*KS) and writes its (value,
     // argmax) partial at C/IDX + y*sY (tg_merge_splits combines them).  An
-    // unsplit launch has gridDim.y == 1, KS == K and sY == 0.
-    const int64_t y = blockIdx.y;
-    C += z * sC + y * sY;
+    // unsplit launch has gridDim.y == 1, KS == K and sY == 0.  With two
+    // halves, half h is slice h (KS == K / 2) and the halves merge in LDS
+    // into C/IDX (sY unused).
+    const int64_t y = HALVES > 1 ? half : int64_t(blockIdx.y);
+    C += z * sC + (HALVES > 1 ? 0 : y * sY);
     if (ARGMAX) {
-        IDX += z * sC + y * sY;
+        IDX += z * sC + (HALVES > 1 ? 0 : y * sY);
         if constexpr (!BDIRECT) BT += z * (N * K);
     }
     // Tile row / column of this thread's output (i, j).
@@ -706,7 +719,7 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
     // The outputs to redo go through a bit mask and one runtime loop, so the
     // serial code is not unrolled per output and does not press on the main
     // loop's registers.
-    const bool split = gridDim.y > 1;
+    const bool split = HALVES > 1 || gridDim.y > 1;
     static_assert(TM * TN <= 64, "one mask bit per output");
     uint64_t redo = 0;
     auto redo_outputs = [&](bool argmax_out) {
@@ -749,10 +762,15 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         // slot, and the thread that owns the output combines them with its
         // own record.
         constexpr uint16_t NONE = 0xFFFF;
-        uint32_t* hist = reinterpret_cast<uint32_t*>(dl_lds + Cfg::HIST_OFF);
-        uint16_t* chs = reinterpret_cast<uint16_t*>(dl_lds + Cfg::CHS_OFF);
-        uint16_t* list = reinterpret_cast<uint16_t*>(dl_lds + Cfg::LIST_OFF);
+        // Two halves: the first half's block holds the one sorted list of the
+        // merged outputs; each half keeps its own scan scratch.
+        constexpr bool H2 = HALVES > 1;
+        unsigned char* const ep_lds = H2 ? dl_lds_all : dl_lds;
+        uint32_t* hist = reinterpret_cast<uint32_t*>(ep_lds + Cfg::HIST_OFF);
+        uint16_t* chs = reinterpret_cast<uint16_t*>(ep_lds + Cfg::CHS_OFF);
+        uint16_t* list = reinterpret_cast<uint16_t*>(ep_lds + Cfg::LIST_OFF);
         int* misc = reinterpret_cast<int*>(dl_lds + Cfg::MISC_OFF);
+        int* const shared_total = reinterpret_cast<int*>(ep_lds + Cfg::MISC_OFF) + 8;
         static_assert(Cfg::MISC_OFF + 64 <= Cfg::LDS_BYTES, "epilogue arrays fit the LDS block");
         static_assert(Cfg::NB <= TG_THREADS, "one bucket per thread in the scan");
         // Buckets: chunk >> shift, at most NB of them.
@@ -768,29 +786,74 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             for (int j = 0; j < TN; ++j)
                 if (tisnan(acc[i][j])) ch[i][j] = -2;
         __syncthreads();  // every wave is done with the tile buffers
-        if (tid < Cfg::NB) hist[tid] = 0;
-        __syncthreads();
+        if constexpr (H2) {
+            // Merge the halves before the resolve, in k order as
+            // tg_merge_splits does: the second slice replaces the first only
+            // if strictly better.  Only the winning slice's chunk is then
+            // resolved, by all 512 threads.  An output that met a NaN product
+            // in either slice (chunk -2) is recomputed at the end.
+            static_assert(2 * TM * TN * TG_THREADS * 4 <= Cfg::LDS_BYTES, "merge buffer fits");
+            T* const mv = reinterpret_cast<T*>(dl_lds_all + Cfg::LDS_BYTES);
+            int32_t* const mi = reinterpret_cast<int32_t*>(mv + TM * TN * TG_THREADS);
+            if (half == 1) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int lid = trow(i) * BN + tcol(j);
-                chs[lid] = ch[i][j] < 0 ? NONE : uint16_t(ch[i][j]);
-                if (ch[i][j] >= 0) atomicAdd(&hist[ch[i][j] >> shift], 1u);
+                    for (int j = 0; j < TN; ++j) {
+                        mv[(i * TN + j) * TG_THREADS + tid] = acc[i][j];
+                        mi[(i * TN + j) * TG_THREADS + tid] = ch[i][j];
+                    }
             }
+            __syncthreads();
+            if (half == 0) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const T v1 = mv[(i * TN + j) * TG_THREADS + tid];
+                        const int32_t c1 = mi[(i * TN + j) * TG_THREADS + tid];
+                        if (ch[i][j] == -2 || c1 == -2) {
+                            ch[i][j] = -2;
+                        } else if (tbetter<SR, T>(v1, acc[i][j])) {
+                            acc[i][j] = v1;
+                            ch[i][j] = c1;
+                        }
+                    }
+            }
+            __syncthreads();  // the merge buffer is free again
+        }
+        const bool sorter = !H2 || half == 0;
+        if (sorter && tid < Cfg::NB) hist[tid] = 0;
+        __syncthreads();
+        if (sorter) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int lid = trow(i) * BN + tcol(j);
+                    chs[lid] = ch[i][j] < 0 ? NONE : uint16_t(ch[i][j]);
+                    if (ch[i][j] >= 0) atomicAdd(&hist[ch[i][j] >> shift], 1u);
+                }
+        }
         __syncthreads();
         // Exclusive scan of the bucket counts; the starts become cursors.
-        const int cnt = tid < nb ? int(hist[tid]) : 0;
+        const int cnt = sorter && tid < nb ? int(hist[tid]) : 0;
         int total = 0;
-        const int start = block_exclusive_scan(cnt, misc, total);
-        if (tid < nb) hist[tid] = uint32_t(start);
+        const int start = block_exclusive_scan(cnt, misc, total, tid);
+        if (sorter && tid < nb) hist[tid] = uint32_t(start);
+        if constexpr (H2) {
+            if (half == 0 && tid == 0) *shared_total = total;
+        }
         __syncthreads();
+        if constexpr (H2) total = *shared_total;
+        if (sorter) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                if (ch[i][j] >= 0)
-                    list[atomicAdd(&hist[ch[i][j] >> shift], 1u)] = uint16_t(trow(i) * BN + tcol(j));
+                for (int j = 0; j < TN; ++j)
+                    if (ch[i][j] >= 0)
+                        list[atomicAdd(&hist[ch[i][j] >> shift], 1u)] = uint16_t(trow(i) * BN + tcol(j));
+        }
         __syncthreads();
 
         // Resolve, chunk-sorted, one output per thread at a time, the next
@@ -860,14 +923,17 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
             }
             chs[int(list[e])] = uint16_t(r);
         };
-        if (tid < total) {
+        // Two halves: all 512 threads resolve the merged list.
+        constexpr int RT = TG_THREADS * HALVES;
+        const int rt = H2 ? int(threadIdx.x) : tid;
+        if (rt < total) {
             Window cur;
-            load_window(tid, cur);
-            for (int e = tid; e < total; e += TG_THREADS) {
+            load_window(rt, cur);
+            for (int e = rt; e < total; e += RT) {
                 // The next entry this thread owns, or this one again (its
                 // chunk slot is overwritten only below): never another
                 // thread's entry, whose slot may already hold an offset.
-                const int en = e + TG_THREADS < total ? e + TG_THREADS : e;
+                const int en = e + RT < total ? e + RT : e;
                 Window nxt;
                 load_window(en, nxt);
                 resolve_entry(e, cur);
@@ -876,31 +942,55 @@ __global__ __launch_bounds__(TG_THREADS) __attribute__((amdgpu_waves_per_eu(
         }
         __syncthreads();
 
+        // Each output's (value, first k) of this slice; acc and ch take them.
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            T v[TN];
-            int32_t ix[TN];
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
+                int32_t ix;
                 if (ch[i][j] == -2) {  // the chain met a NaN product: redone below
-                    v[j] = acc[i][j];
-                    ix[j] = 0;
+                    ix = 0;
                     redo |= uint64_t(1) << (i * TN + j);
                 } else if (ch[i][j] < 0) {  // the tropical zero was never beaten
-                    v[j] = tzero<SR, T>();
-                    ix[j] = 0;
+                    acc[i][j] = tzero<SR, T>();
+                    ix = 0;
                 } else {
                     const int r = chs[trow(i) * BN + tcol(j)];
-                    ix[j] = ch[i][j] * CL + (r & 31);
-                    v[j] = acc[i][j];
+                    ix = ch[i][j] * CL + (r & 31);
                     if constexpr (std::is_floating_point<T>::value) {
-                        if (v[j] == T(0)) v[j] = (r & 32) ? -T(0) : T(0);
+                        if (acc[i][j] == T(0)) acc[i][j] = (r & 32) ? -T(0) : T(0);
                     }
                 }
+                ch[i][j] = ix;
             }
-            store_row(i, v, ix);
+        if constexpr (H2) {
+            // The first half holds the merged outputs; a NaN in either slice
+            // is recomputed with the reference's serial rule over the whole
+            // k range (the unsplit kernel's redo, which a split slice skips).
+            if (half == 0) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) store_row(i, acc[i], ch[i]);
+#pragma unroll 1
+                while (redo) {
+                    const int o = __builtin_ctzll(redo);
+                    redo &= redo - 1;
+                    const int64_t gr = row0 + trow(o / TN), gc = col0 + tcol(o % TN);
+                    if (gr >= M || gc >= N) continue;
+                    T v;
+                    int32_t ix;
+                    if (!BDIRECT)
+                        cpu_select<SR, T>(A + gr * K, 1, BT + gc * K, 1, K, v, ix);
+                    else
+                        cpu_select<SR, T>(A + gr * K, 1, B + gc, N, K, v, ix);
+                    C[gr * N + gc] = v;
+                    IDX[gr * N + gc] = ix;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) store_row(i, acc[i], ch[i]);
+            if constexpr (std::is_floating_point<T>::value) redo_outputs(true);
         }
-        if constexpr (std::is_floating_point<T>::value) redo_outputs(true);
     }
 }
 
