@@ -356,12 +356,23 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
             TG_HIP(attr_pipe);
         }
     }
-    // Argmax with two K slices on 64 x 64 tiles: one 512-thread workgroup per
-    // tile, each 256-thread half running one slice, merged in LDS (no
-    // partials, no merge launch).
+    // Split argmax on 64 x 64 tiles: the K slices of a tile run in one
+    // workgroup, 256 threads per slice, and merge in LDS (no partials, no
+    // merge launch).  Four slices (1024 threads, four waves per SIMD) when
+    // each slice keeps at least 256 k, else two.
     constexpr bool kHalves = TM == 4 && TN == 4 && (Cfg::BK / CL) % 2 == 0;
-    if (kHalves && argmax && splits == 2 && p.K % (2 * Cfg::BK) == 0) {
+    if (kHalves && argmax && (splits == 2 || splits == 4) && p.K % (2 * Cfg::BK) == 0) {
         if constexpr (kHalves) {
+            const int halves = (p.K % (4 * Cfg::BK) == 0 && p.K / 4 >= 256) ? 4 : 2;
+            const int64_t KSh = p.K / halves;
+            static const hipError_t attr4 = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, false, 0, 4>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * Cfg::LDS_BYTES);
+            static const hipError_t attr4d = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, true, 0, 4>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, 4 * Cfg::LDS_BYTES);
+            TG_HIP(attr4);
+            TG_HIP(attr4d);
             KernelTimer timer(st);
             for (int64_t z0 = 0; z0 < p.batch; z0 += 65535) {
                 const int64_t nb = (p.batch - z0 < 65535) ? p.batch - z0 : 65535;
@@ -371,16 +382,28 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
                 int32_t* Iz = p.IDX + z0 * p.sC;
                 const T* BT = reinterpret_cast<const T*>(wsb + wl.bt) + z0 * p.K * p.N;
                 dim3 grid(unsigned(tiles_m * tiles_n), 1, unsigned(nb));
-                if (bdirect)
+                if (halves == 4) {
+                    if (bdirect)
+                        hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, true, 0, 4>),
+                                           grid, dim3(1024), 4 * Cfg::LDS_BYTES, st, Az, Bz, nullptr,
+                                           Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                                           int(tiles_n), KSh, int64_t(0));
+                    else
+                        hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, false, 0, 4>),
+                                           grid, dim3(1024), 4 * Cfg::LDS_BYTES, st, Az, Bz, BT, Cz,
+                                           Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
+                                           int(tiles_n), KSh, int64_t(0));
+                } else if (bdirect) {
                     hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, true, 0, 2>),
                                        grid, dim3(512), 2 * Cfg::LDS_BYTES, st, Az, Bz, nullptr, Cz,
                                        Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m),
-                                       int(tiles_n), KS, int64_t(0));
-                else
+                                       int(tiles_n), KSh, int64_t(0));
+                } else {
                     hipLaunchKernelGGL((tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, false, 0, 2>),
                                        grid, dim3(512), 2 * Cfg::LDS_BYTES, st, Az, Bz, BT, Cz, Iz,
                                        p.M, p.N, p.K, p.sA, p.sB, p.sC, int(tiles_m), int(tiles_n),
-                                       KS, int64_t(0));
+                                       KSh, int64_t(0));
+                }
                 TG_HIP(hipGetLastError());
             }
         }

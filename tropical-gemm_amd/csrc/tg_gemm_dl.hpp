@@ -317,13 +317,13 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
     static_assert(CL == 8 || CL == 16 || CL == 32, "argmax chunk of 8, 16 or 32 k");
     static_assert(!ARGMAX || (BK / CL) % 2 == 0, "argmax: an even number of chunks per k-tile");
     static_assert(!ARGMAX || TM == 4, "argmax tiles have 4 rows per thread");
-    static_assert(HALVES == 1 || (HALVES == 2 && ARGMAX && !TAILK && PIPE == 0),
-                  "two K slices per workgroup: argmax, whole k-tiles");
+    static_assert(HALVES == 1 || ((HALVES == 2 || HALVES == 4) && ARGMAX && !TAILK && PIPE == 0),
+                  "K slices per workgroup (2 or 4): argmax, whole k-tiles");
     extern __shared__ __align__(16) unsigned char dl_lds_all[];
-    // HALVES == 2: the workgroup is two 256-thread halves, each running the
-    // whole kernel on its own K slice with its own LDS block; they meet
-    // only at the barriers (every barrier is reached by both) and in the
-    // merge at the end.
+    // HALVES > 1: the workgroup is HALVES 256-thread parts ("halves" for
+    // short), each running the kernel on its own K slice with its own LDS
+    // block; they meet only at the barriers (every barrier is reached by
+    // all of them) and in the merge before the resolve.
     const int half = HALVES > 1 ? int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 8)) : 0;
     unsigned char* const dl_lds = dl_lds_all + (HALVES > 1 ? half * Cfg::LDS_BYTES : 0);
     T* const As0 = reinterpret_cast<T*>(dl_lds);
@@ -343,9 +343,9 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
     B += z * sB;
     // Split K: slice y covers k in [y*KS, (y+1)*KS) and writes its (value,
     // argmax) partial at C/IDX + y*sY (tg_merge_splits combines them).  An
-    // unsplit launch has gridDim.y == 1, KS == K and sY == 0.  With two
-    // halves, half h is slice h (KS == K / 2) and the halves merge in LDS
-    // into C/IDX (sY unused).
+    // unsplit launch has gridDim.y == 1, KS == K and sY == 0.  With
+    // halves, half h is slice h (KS == K / HALVES) and the halves merge in
+    // LDS into C/IDX (sY unused).
     const int64_t y = HALVES > 1 ? half : int64_t(blockIdx.y);
     C += z * sC + (HALVES > 1 ? 0 : y * sY);
     if (ARGMAX) {
@@ -762,7 +762,7 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
         // slot, and the thread that owns the output combines them with its
         // own record.
         constexpr uint16_t NONE = 0xFFFF;
-        // Two halves: the first half's block holds the one sorted list of the
+        // Halves: the first half's block holds the one sorted list of the
         // merged outputs; each half keeps its own scan scratch.
         constexpr bool H2 = HALVES > 1;
         unsigned char* const ep_lds = H2 ? dl_lds_all : dl_lds;
@@ -788,14 +788,15 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
         __syncthreads();  // every wave is done with the tile buffers
         if constexpr (H2) {
             // Merge the halves before the resolve, in k order as
-            // tg_merge_splits does: the second slice replaces the first only
-            // if strictly better.  Only the winning slice's chunk is then
-            // resolved, by all 512 threads.  An output that met a NaN product
-            // in either slice (chunk -2) is recomputed at the end.
+            // tg_merge_splits does: a later slice replaces the running result
+            // only if strictly better.  Only the winning slice's chunk is
+            // then resolved, by all the workgroup's threads.  An output that
+            // met a NaN product in any slice (chunk -2) is recomputed at the
+            // end.  Halves 1.. hand over through their own LDS blocks.
             static_assert(2 * TM * TN * TG_THREADS * 4 <= Cfg::LDS_BYTES, "merge buffer fits");
-            T* const mv = reinterpret_cast<T*>(dl_lds_all + Cfg::LDS_BYTES);
-            int32_t* const mi = reinterpret_cast<int32_t*>(mv + TM * TN * TG_THREADS);
-            if (half == 1) {
+            if (half > 0) {
+                T* const mv = reinterpret_cast<T*>(dl_lds);
+                int32_t* const mi = reinterpret_cast<int32_t*>(mv + TM * TN * TG_THREADS);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -806,21 +807,27 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
             }
             __syncthreads();
             if (half == 0) {
+#pragma unroll 1
+                for (int h = 1; h < HALVES; ++h) {
+                    const T* const mv = reinterpret_cast<const T*>(dl_lds_all + h * Cfg::LDS_BYTES);
+                    const int32_t* const mi =
+                        reinterpret_cast<const int32_t*>(mv + TM * TN * TG_THREADS);
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                    for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        const T v1 = mv[(i * TN + j) * TG_THREADS + tid];
-                        const int32_t c1 = mi[(i * TN + j) * TG_THREADS + tid];
-                        if (ch[i][j] == -2 || c1 == -2) {
-                            ch[i][j] = -2;
-                        } else if (tbetter<SR, T>(v1, acc[i][j])) {
-                            acc[i][j] = v1;
-                            ch[i][j] = c1;
+                        for (int j = 0; j < TN; ++j) {
+                            const T v1 = mv[(i * TN + j) * TG_THREADS + tid];
+                            const int32_t c1 = mi[(i * TN + j) * TG_THREADS + tid];
+                            if (ch[i][j] == -2 || c1 == -2) {
+                                ch[i][j] = -2;
+                            } else if (tbetter<SR, T>(v1, acc[i][j])) {
+                                acc[i][j] = v1;
+                                ch[i][j] = c1;
+                            }
                         }
-                    }
+                }
             }
-            __syncthreads();  // the merge buffer is free again
+            __syncthreads();  // the merge buffers are free again
         }
         const bool sorter = !H2 || half == 0;
         if (sorter && tid < Cfg::NB) hist[tid] = 0;
@@ -923,7 +930,7 @@ __global__ __launch_bounds__(TG_THREADS * HALVES) __attribute__((amdgpu_waves_pe
             }
             chs[int(list[e])] = uint16_t(r);
         };
-        // Two halves: all 512 threads resolve the merged list.
+        // Halves: all the workgroup's threads resolve the merged list.
         constexpr int RT = TG_THREADS * HALVES;
         const int rt = H2 ? int(threadIdx.x) : tid;
         if (rt < total) {
