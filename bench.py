@@ -69,7 +69,7 @@ WORKLOAD_NAMES = {
 }
 KERNEL_NAMES = {
     "P": "tg_gemm_dl<MaxPlus, f32, argmax>",
-    "C1": "tg_gemm_dl<MaxPlus, f32, argmax> split-K x2 + tg_merge_splits",
+    "C1": "tg_gemm_dl<MaxPlus, f32, argmax> 4 K slices in one 1024-thread workgroup per 64x64 tile",
     "C2": "tg_gemm_dl<MinPlus, f32, argmax>",
     "C3": "tg_gemm_dl<MaxMul, f32, value-only>",
     "C4": "tg_gemm_kresw<MaxPlus, K=128> (wave-private 16x128 tiles, f32 keys)",
@@ -85,10 +85,9 @@ KERNEL_NAMES = {
 # (profiles/tg_gemm_dl_maxplus_f32_4096_argmax.md, profiles/tg_gemm_kresw_*.md,
 # profiles/tg_gemm_shortk_*.md, profiles/hbm_traffic_c2_c3_e1.md,
 # profiles/tg_gemm_dl_split_*.md, profiles/tg_gemm_dl64_*.md,
-# profiles/tg_gemm_tiles_maxplus_i64_4096.md).  E1: per GEMM launch; C1: the
-# split GEMM launch (the merge adds 0.025e9).
+# profiles/tg_gemm_tiles_maxplus_i64_4096.md).  E1: per GEMM launch.
 
-TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.418e9, "M1": 1.108e9, "C1": 0.042e9,
+TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.418e9, "M1": 1.108e9, "C1": 0.034e9,
            "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9,
            "I1": 7.997e9, "I2": 3.356e9}
 
