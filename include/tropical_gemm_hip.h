@@ -133,8 +133,10 @@ size_t tg_gemm_workspace_size(tg_dtype dtype, int64_t batch, int64_t m, int64_t 
 
 /* Name of the kernel path tg_gemm_ws would run for this problem with a
  * workspace of workspace_bytes (tg_gemm passes tg_gemm_workspace_size), e.g.
- * "dl_4x8_cl16", "shortk", "tiles_exact" or "dl_4x4_cl8 split 2"; "invalid"
- * for arguments the call would reject, "none" for an empty product.  Strides
+ * "dl_4x8_cl16", "shortk", "tiles_exact", "dl_4x4_cl32 split 4" (K in four
+ * launches merged afterwards) or "dl_4x4_cl8 slices 4" (four K slices in one
+ * workgroup per tile); "invalid" for arguments the call would reject, "none"
+ * for an empty product.  Strides
  * 0 mean dense single products.  Pure host logic: pointers are only checked
  * for alignment, never dereferenced, and no device is needed.  Diagnostic,
  * with no counterpart in the reference (which has one kernel per dtype). */

@@ -126,7 +126,7 @@ def test_python_layer_rejects_host_tensors():
     ("minplus", "f32", 4096, 4096, 4096, True, "dl_4x8_cl16"),       # C2
     ("maxmul", "f32", 8192, 4096, 2048, False, "dl_8x8_cl32"),       # C3
     ("maxplus", "i32", 262144, 128, 128, True, "kresw"),             # C4
-    ("maxplus", "f32", 1024, 1024, 1024, True, "dl_4x4_cl8 split 2"),  # C1
+    ("maxplus", "f32", 1024, 1024, 1024, True, "dl_4x4_cl8 slices 4"),  # C1
     ("maxplus", "f32", 65536, 8, 2048, True, "shortk"),              # M1 (m, k, n order below)
     ("maxplus", "f32", 67, 45, 40, True, "tiles_exact"),
     ("maxplus", "f64", 4096, 4096, 4096, True, "dl64_4x8_cl16"),
@@ -198,7 +198,7 @@ def test_noalloc_bytes_of_other_paths():
     assert _noalloc_bytes("maxplus", "f32", 4096, 4096, 4096, True) == 4096 * 4096 * 4
     # Split K: the value and index partials after the (here unused) B^T region.
     assert nat.gemm_plan("maxplus", "f32", 1024, 1024, 1024, True,
-                         workspace_bytes=64 << 20) == "dl_4x4_cl8 split 2"
+                         workspace_bytes=64 << 20) == "dl_4x4_cl8 slices 4"
     assert _noalloc_bytes("maxplus", "f32", 1024, 1024, 1024, True) == \
         1024 * 1024 * 4 + 2 * (2 * 1024 * 1024 * 4)
     # Paths without workspace, and empty products.

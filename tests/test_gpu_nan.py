@@ -95,8 +95,8 @@ CASES = [
     ("maxmul", "f64", 64, 64, 640, True, "alloc", "tiles_chunked"),
     ("maxplus", "f64", 64, 64, 640, False, "alloc", "tiles"),
     ("maxmul", "f64", 64, 64, 640, False, "alloc", "tiles"),
-    ("maxplus", "f32", 256, 256, 1024, True, "ws", "dl_4x4_cl8 split 4"),
-    ("minplus", "f32", 256, 256, 1024, True, "ws", "dl_4x4_cl8 split 4"),
+    ("maxplus", "f32", 256, 256, 1024, True, "ws", "dl_4x4_cl8 slices 4"),
+    ("minplus", "f32", 256, 256, 1024, True, "ws", "dl_4x4_cl8 slices 4"),
     ("maxplus", "f32", 256, 256, 1024, False, "ws", "dl_4x4_cl32 split 4"),
     ("maxplus", "f32", 256, 256, 1024, True, "min", "dl_4x4_cl16"),
     ("maxmul", "f32", 256, 256, 512, True, "min", "dl_4x4_cl8"),

@@ -59,7 +59,7 @@ def test_noalloc_bad_arguments_rejected():
 CASES = [
     ("maxplus", "f32", "row", True, (2048, 2048, 2048), (256, 256, 1024), "dl_4x4_cl16"),
     ("maxplus", "f32", "row", True, (512, 512, 2048), (256, 256, 1024), "dl_4x4_cl8 split 8"),
-    ("minplus", "f32", "row", True, (256, 256, 1024), (128, 192, 640), "dl_4x4_cl8 split 4"),
+    ("minplus", "f32", "row", True, (256, 256, 1024), (128, 192, 640), "dl_4x4_cl8 slices 4"),
     ("maxplus", "f32", "row", False, (256, 256, 1024), (128, 128, 512), "dl_4x4_cl32 split 4"),
     ("maxmul", "f64", "row", True, (64, 130, 640), (40, 64, 320), "tiles_chunked"),
     ("maxplus", "f64", "row", True, (1024, 4096, 640), (1024, 2048, 576), "dl64_4x8_cl16"),

@@ -302,6 +302,16 @@ int run_gemm_dl64(const Problem& p, void* ws, hipStream_t st) {
     return TG_OK;
 }
 
+// Split argmax on 64 x 64 tiles whose chunk holds an even number of
+// fragments runs its K slices in one workgroup: the number of slices (four
+// when each keeps at least 256 k, else two), or 0 when the split runs as
+// separate launches into the workspace partials.
+inline int wg_slices(bool slices_ok, bool argmax, int splits, int64_t K) {
+    constexpr int BK = tg::TG_CHUNK;
+    if (!slices_ok || !argmax || (splits != 2 && splits != 4) || K % (2 * BK) != 0) return 0;
+    return (K % (4 * BK) == 0 && K / 4 >= 256) ? 4 : 2;
+}
+
 // Direct-to-LDS kernel for 32-bit types (partial edge tiles allowed, see
 // tg::dl_fits).  splits > 1 (full tiles only) runs K in that many slices into
 // the workspace partials, then merges them.
@@ -361,9 +371,8 @@ int run_gemm_dl(const Problem& p, void* ws, int splits, hipStream_t st) {
     // merge launch).  Four slices (1024 threads, four waves per SIMD) when
     // each slice keeps at least 256 k, else two.
     constexpr bool kHalves = TM == 4 && TN == 4 && (Cfg::BK / CL) % 2 == 0;
-    if (kHalves && argmax && (splits == 2 || splits == 4) && p.K % (2 * Cfg::BK) == 0) {
+    if (const int halves = wg_slices(kHalves, argmax, splits, p.K)) {
         if constexpr (kHalves) {
-            const int halves = (p.K % (4 * Cfg::BK) == 0 && p.K / 4 >= 256) ? 4 : 2;
             const int64_t KSh = p.K / halves;
             static const hipError_t attr4 = hipFuncSetAttribute(
                 reinterpret_cast<const void*>(&tg::tg_gemm_dl<SR, T, true, TM, TN, CL, false, false, 0, 4>),
@@ -1621,7 +1630,11 @@ const char* tg_gemm_plan(tg_semiring semiring, tg_dtype dtype, tg_layout layout,
                                    batch, m, n, k, stride_a, stride_b, stride_c, strided);
     const Plan pl = plan_gemm(semiring, dtype, p, workspace_bytes);
     name = path_name(pl.path);
-    if (pl.splits > 1) name += " split " + std::to_string(pl.splits);
+    const bool slices_ok = pl.path == Path::DL_44_8 || pl.path == Path::DL_44_16;
+    if (const int s = wg_slices(slices_ok, argmax != nullptr, pl.splits, p.K))
+        name += " slices " + std::to_string(s);
+    else if (pl.splits > 1)
+        name += " split " + std::to_string(pl.splits);
     return name.c_str();
 }
 
