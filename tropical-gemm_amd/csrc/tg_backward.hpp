@@ -176,6 +176,21 @@ __device__ __forceinline__ void stage_clear(T* stage) {
     asm volatile("" ::: "memory");
 }
 
+// Zeroes this wave's n LDS bins, one 16-byte store per lane and step when n
+// is a multiple of the vector (the bins then start 16-byte aligned: the
+// stages and every wave's bins before them are whole vectors).
+template <typename T>
+__device__ __forceinline__ void bins_zero(T* bins, int64_t n) {
+    constexpr int E = 16 / sizeof(T);
+    typedef T V __attribute__((ext_vector_type(E)));
+    const int lane = threadIdx.x & 63;
+    if (n % E == 0) {
+        for (int64_t k = int64_t(lane) * E; k < n; k += 64 * E) *reinterpret_cast<V*>(bins + k) = V(T(0));
+    } else {
+        for (int64_t k = lane; k < n; k += 64) bins[k] = T(0);
+    }
+}
+
 // bins[key] += g in lane order among equal keys, bins in LDS.  Wave-uniform.
 template <typename T>
 __device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active) {
@@ -248,7 +263,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
                 __hip_atomic_store(bins + k, T(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __threadfence();  // zeros visible to every lane's first read
         } else {
-            for (int64_t k = lane; k < K; k += 64) bins[k] = T(0);
+            bins_zero(bins, K);
         }
         // Contributions in chunks of PF blocks of 64 consecutive j.  The next
         // chunk's loads are issued before the current chunk is applied
@@ -290,8 +305,17 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
         }
         if constexpr (!GLOBAL) {
             // The row leaves as one contiguous run: non-temporal stores took
-            // 1-3 us off grad_A at 4096^3 on every index pattern tried.
-            for (int64_t k = lane; k < K; k += 64) __builtin_nontemporal_store(bins[k], out + k);
+            // 1-3 us off grad_A at 4096^3 on every index pattern tried, and
+            // 16-byte ones (with the 16-byte zeroing above) another 5-6 us.
+            constexpr int E = 16 / sizeof(T);
+            typedef T V __attribute__((ext_vector_type(E)));
+            if (K % E == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+                for (int64_t k = int64_t(lane) * E; k < K; k += 64 * E)
+                    __builtin_nontemporal_store(*reinterpret_cast<const V*>(bins + k),
+                                                reinterpret_cast<V*>(out + k));
+            } else {
+                for (int64_t k = lane; k < K; k += 64) __builtin_nontemporal_store(bins[k], out + k);
+            }
         }
     }
 }
@@ -364,7 +388,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 __threadfence();
             } else {
-                for (int64_t k = lane; k < K; k += 64) bins[k] = T(0);
+                bins_zero(bins, K);
             }
         }
         const int64_t cc = c0 + sq;
@@ -412,9 +436,25 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
         if constexpr (!GLOBAL) {
             __syncthreads();  // every wave's bins are complete
             // The W columns leave together: row k of the group is W
-            // consecutive elements of grad_B.  blockDim = 64 W, so thread tid
-            // writes column q = tid % W of rows tid / W, + 64, + 128, ...
-            if (c0 + sq < N) {
+            // consecutive elements of grad_B.  A whole group of 8 columns
+            // whose rows start 16-byte aligned leaves in 16-byte stores, 8 / E
+            // threads per row, each gathering E columns from their bins;
+            // otherwise blockDim = 64 W, and thread tid writes column
+            // q = tid % W of rows tid / W, + 64, + 128, ...
+            constexpr int E = 16 / sizeof(T);
+            typedef T V __attribute__((ext_vector_type(E)));
+            const bool vec = W == 8 && c0 + W <= N && N % E == 0 &&
+                             (reinterpret_cast<uintptr_t>(outz) & 15) == 0;
+            if (vec) {
+                constexpr int TPR = 8 / E;
+                const int q0 = (tid % TPR) * E;
+                for (int64_t k = tid / TPR; k < K; k += 512 / TPR) {
+                    V v;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) v[e] = bins_all[int64_t(q0 + e) * K + k];
+                    *reinterpret_cast<V*>(outz + k * N + c0 + q0) = v;
+                }
+            } else if (c0 + sq < N) {
                 const T* src = bins_all + int64_t(sq) * K;
                 T* dst = outz + c0 + sq;
                 for (int64_t k = sr; k < K; k += 64) dst[k * N] = src[k];
