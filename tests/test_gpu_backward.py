@@ -47,10 +47,11 @@ def test_backward_matches_oracle(dtype, sr, shape):
     assert_bits(gb, oracle.backward_b(g, am, k, a if mult else None))
 
 
-# Argmax patterns that steer the kernels down each of their paths: spread
-# indices (one round per block), paired and clustered indices (several
-# rounds), indices that repeat more than kRoundsMax times per block (the
-# serial per-bin sums), and the argmax of N(0,1) data.
+# Argmax patterns that steer the LDS-bin kernels down each of their paths:
+# spread indices (lanes alone with their bin: a plain read-add-write), paired
+# and clustered indices (shared bins: ordered LDS float atomics), one or four
+# bins per block (rows and columns on atomics alone), and the argmax of
+# N(0,1) data (about half the lanes of a block share a bin).
 PATTERNS = ["uniform", "all zero", "four values", "k = j", "pairs", "row argmax"]
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("pattern", PATTERNS)
@@ -85,6 +86,48 @@ def test_backward_index_patterns(dtype, pattern):
     # Run to run: the same bits again.
     assert_bits(ops.backward_a(tg, tam, k).cpu().numpy(), ga)
     assert_bits(ops.backward_b(tg, tam, k).cpu().numpy(), gb)
+
+
+# Sums whose bits depend on every rounding step, on the LDS-bin kernels
+# (ordered LDS float atomics where lanes of a block share a bin, a plain
+# read-add-write where a lane is alone with it): contributions of mixed
+# magnitudes (2^-30 .. 2^30), round-to-even ties (1.0 among halves of an
+# ulp), denormal values and cancellations into the denormal range.  Rows
+# (and columns) whose first block is one bin run on atomics alone, the others
+# count first: rows 0 mod 3 start with a one-bin block and then spread, rows
+# 1 mod 3 start spread and then use three bins, and the first 64 rows of
+# every fifth column are one bin.
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_backward_rounding_denormals_and_modes(dtype):
+    from tropical_gemm import ops
+
+    m, n, k = 160, 2048, 512
+    rng = np.random.default_rng(77)
+    fi = np.finfo(dtype)
+    g = rng.standard_normal((m, n)) * np.exp2(rng.integers(-30, 31, size=(m, n)))
+    g[:48] = np.where(rng.random((48, n)) < 0.1, 1.0,
+                      fi.eps / 2 * rng.integers(1, 4, size=(48, n)) * rng.choice([-1, 1], size=(48, n)))
+    g[48:96] = rng.uniform(0.5, 1, size=(48, n)) * rng.choice([-1, 1], size=(48, n)) * float(
+        fi.tiny) * np.exp2(rng.integers(-20, 4, size=(48, n)))
+    g = g.astype(dtype)
+    assert (np.abs(g[48:96]) < fi.tiny).any() and (g[48:96] != 0).all()  # denormal contributions
+    am = rng.integers(0, k, size=(m, n))
+    for i in range(m):
+        if i % 3 == 0:
+            am[i, :64] = 7
+        elif i % 3 == 1:
+            am[i, 64:] = rng.integers(0, 3, size=n - 64)
+    am[:64, ::5] = 11
+    print(f"[case] backward rounding/denormals {np.dtype(dtype).name}", flush=True)
+    tg = torch.from_numpy(g).to(DEV)
+    tam = torch.from_numpy(am.astype(np.int32)).to(DEV)
+    ga = ops.backward_a(tg, tam, k).cpu().numpy()
+    gb = ops.backward_b(tg, tam, k).cpu().numpy()
+    ref_a = oracle.backward_a(g, am.astype(np.uint32), k)
+    ref_b = oracle.backward_b(g, am.astype(np.uint32), k)
+    assert ((np.abs(ref_a[48:96]) < fi.tiny) & (ref_a[48:96] != 0)).any()  # denormal sums
+    assert_bits(ga, ref_a)
+    assert_bits(gb, ref_b)
 
 
 def test_backward_column_major_and_out_of_range_index():

@@ -12,27 +12,40 @@
 // is bit-identical to the reference and the same from run to run.
 //
 // Ordering inside a wave: a block of 64 consecutive contributions (one per
-// lane, in lane order) is grouped by target bin, and the lowest lane of each
-// group (its leader) applies the group: bin + g(leader) + g(2nd) + ... in
-// lane order, one read and one write of the bin.  Groups have distinct bins,
-// so they run side by side; blocks run in sequence.
-//   * Grouping with LDS bins (lds_group): every active lane saves its bin's
-//     value, zeroes the bin, ORs its lane bit into it and reads it back,
-//     which leaves each lane the mask of the lanes sharing its bin (f32 bins
-//     hold 32 bits: two halves of the wave in turn; f64 bins one 64-bit OR).
-//     Seven (four) LDS instructions, one round trip.  With bins in global
-//     memory (K too large for LDS) the mask comes from 64-bit ballots over
-//     the bits of the bin index instead (wave_match_mask).
-//   * Summing (group_sum): in passes of kStageRanks ranks, each member of
-//     rank r0 + u posts its value to slot u of its leader's kStageRanks
-//     contiguous slots in a per-wave LDS stage, and each leader whose group
-//     reaches rank r0 reads its slots with one vector load: kStageRanks
-//     values, the missing ranks +0.0.  Adding +0.0 never changes a running
-//     sum that starts from +0.0 (such a sum is never -0.0 under
-//     round-to-nearest), so the leader adds every slot unconditionally.  It
-//     clears its slots behind it, so the stage is all +0.0 between passes;
-//     no other lane touches the stage, which keeps the LDS work of a pass
-//     proportional to the groups that need it.
+// lane, in lane order) is applied to its bins in lane order; blocks run in
+// sequence.
+//   * Bins in LDS (lds_apply): LDS float atomic adds (ds_add_f32 /
+//     ds_add_f64, no return) apply the lanes of one instruction that hit
+//     the same address in lane order, each an IEEE add rounded to nearest
+//     even with denormals kept, and a wave's LDS instructions execute in
+//     order.  Measured on gfx950 against the sequential sum in lane order:
+//     bit-equal over random keys (1 to 64 distinct per block), mixed
+//     magnitudes, round-to-even ties, denormal values and sums, signed
+//     zeros, infinities and NaN positions, within one instruction and across
+//     consecutive ones.  So one atomic per contribution keeps the
+//     reference's order.  The LDS serves these atomics about one lane per
+//     2.6 clocks per CU, about 30x slower than integer adds, so a block first
+//     counts its lanes per hash of the bin (a per-wave table of kCountSlots
+//     integer counters: add, read back, clear), and only lanes whose hash
+//     is shared take the atomic; a lane alone with its hash (so alone with
+//     its bin) adds with a plain read and write.  A row (column) whose first
+//     block has more than kAllSharedAbove shared lanes is applied with
+//     atomics only: the count would not spare any.
+//   * Bins in global memory (K too large for LDS: global_apply): the lanes
+//     sharing a bin are found by 64-bit ballots over the bits of the bin
+//     index (wave_match_mask), and the lowest lane of each group (its
+//     leader) applies the group: bin + g(leader) + g(2nd) + ... in lane
+//     order, one read and one write of the bin.  Groups have distinct bins,
+//     so they run side by side.  Summing (group_sum): in passes of
+//     kStageRanks ranks, each member of rank r0 + u posts its value to slot
+//     u of its leader's kStageRanks contiguous slots in a per-wave LDS stage,
+//     and each leader whose group reaches rank r0 reads its slots with one
+//     vector load: kStageRanks values, the missing ranks +0.0.  Adding +0.0
+//     never changes a running sum that starts from +0.0 (such a sum is never
+//     -0.0 under round-to-nearest), so the leader adds every slot
+//     unconditionally.  It clears its slots behind it, so the stage is all
+//     +0.0 between passes; no other lane touches the stage, which keeps the
+//     LDS work of a pass proportional to the groups that need it.
 //
 #pragma once
 
@@ -59,8 +72,9 @@ __host__ __device__ inline int key_bits(int64_t K) {
     return b;
 }
 
-// Relaxed LDS accesses for the grouping steps: atomics, so the compiler
-// keeps every step (no store-to-load forwarding across another lane's OR).
+// Relaxed LDS accesses for the counters and bins that other lanes of the
+// wave update: atomics, so the compiler keeps every access (no
+// store-to-load forwarding across another lane's add).
 template <typename U>
 __device__ __forceinline__ U lds_ld(U* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
@@ -69,55 +83,22 @@ template <typename U>
 __device__ __forceinline__ void lds_st(U* p, U v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
-template <typename U>
-__device__ __forceinline__ void lds_or(U* p, U v) {
-    __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-}
-
-// Groups the active lanes by LDS bin (see the header comment): returns the
-// mask of the active lanes whose key equals this lane's (0 when inactive)
-// and the bin's value before this block in `before`.  Inactive lanes run the
-// same steps on their own dummy slot, so no step needs an exec mask.  Leaves
-// garbage in the touched bins: the leaders overwrite them (lds_apply).
+// LDS float add, no return (ds_add_f32 / ds_add_f64): same-address lanes of
+// one instruction are applied in lane order (see the header comment).
 template <typename T>
-__device__ __forceinline__ uint64_t lds_group(T* bins, T* dummy, int32_t key, bool active,
-                                              T& before) {
-    const int lane = threadIdx.x & 63;
-    T* const target = active ? bins + key : dummy + lane;
-    if constexpr (sizeof(T) == 8) {
-        uint64_t* slot = reinterpret_cast<uint64_t*>(target);
-        before = __builtin_bit_cast(T, lds_ld(slot));
-        lds_st(slot, uint64_t(0));
-        lds_or(slot, uint64_t(1) << lane);
-        const uint64_t m = lds_ld(slot);
-        return active ? m : 0;
-    } else {
-        // Each half of the wave ORs its bits in turn; the other half ORs into
-        // its own dummy slot meanwhile (atomics on one address serialize).
-        uint32_t* slot = reinterpret_cast<uint32_t*>(target);
-        uint32_t* spare = reinterpret_cast<uint32_t*>(dummy + lane);
-        const uint32_t bit = 1u << (lane & 31);
-        before = __builtin_bit_cast(T, lds_ld(slot));
-        lds_st(slot, 0u);
-        lds_or(lane < 32 ? slot : spare, bit);
-        const uint32_t lo = lds_ld(slot);
-        lds_st(slot, 0u);
-        lds_or(lane < 32 ? spare : slot, bit);
-        const uint32_t hi = lds_ld(slot);
-        return active ? (uint64_t(hi) << 32) | lo : 0;
-    }
+__device__ __forceinline__ void lds_fadd(T* p, T v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
-// Ranks per stage pass.  A wave's stage: 64 leaders x kStageRanks slots,
-// then 64 dummy slots, one per lane (the targets of inactive lanes and of
-// non-leaders, so the grouping and the apply run without exec masks).
-// Passes per wait (group_sum): 2 took C5-like argmax (MaxPlus f32 4096^3)
-// from 129 to 122 us for grad_A and 158 to 148 us for grad_B against 1 pass;
-// 4 was slower on uniformly random indices.
+// Ranks per stage pass.  A wave's stage: 64 leaders x kStageRanks slots
+// (with LDS bins: the block's counters instead).  Passes per wait
+// (group_sum): 2 took C5-like argmax (MaxPlus f32 4096^3) from 129 to 122 us
+// for grad_A and 158 to 148 us for grad_B against 1 pass; 4 was slower on
+// uniformly random indices.
 constexpr int kStageRanks = 4;
 constexpr int kStagePasses = 2;
 constexpr int kStageSlots = kStageRanks * 64;
-constexpr int kStageElems = kStageSlots + 64;
+constexpr int kStageElems = kStageSlots;
 
 // The leader's sum before + g(leader) + g(rank 1) + g(rank 2) + ... of its
 // group (m: this lane's group mask, 0 when inactive); meaningful on leaders
@@ -167,7 +148,8 @@ __device__ __forceinline__ T group_sum(uint64_t m, T g, T before, bool& leader, 
     return acc;
 }
 
-// Zeroes the slots of this wave's stage.
+// Zeroes the slots of this wave's stage (which holds at least kCountSlots
+// 32-bit counters).
 template <typename T>
 __device__ __forceinline__ void stage_clear(T* stage) {
     const int lane = threadIdx.x & 63;
@@ -191,16 +173,36 @@ __device__ __forceinline__ void bins_zero(T* bins, int64_t n) {
     }
 }
 
-// bins[key] += g in lane order among equal keys, bins in LDS.  Wave-uniform.
+// LDS bins: counters per wave (in its stage, zero between blocks) and the
+// shared-lane count above which a row or column runs on atomics alone.
+constexpr int kCountSlots = 256;
+constexpr int kAllSharedAbove = 48;
+static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
+              "the counters fit a wave's stage");
+
+// bins[key] += g in lane order among equal keys, bins in LDS (see the header
+// comment).  mode: -1 before a row's (column's) first block, which sets it
+// to 1 (atomics only) or 0 (count first).  Wave-uniform.
 template <typename T>
-__device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active) {
-    const int lane = threadIdx.x & 63;
-    T* const dummy = stage + kStageSlots;
-    T before;
-    const uint64_t m = lds_group(bins, dummy, key, active, before);
-    bool leader;
-    const T acc = group_sum(m, g, before, leader, stage);
-    lds_st(leader ? bins + key : dummy + lane, acc);
+__device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active,
+                                          int& mode) {
+    if (mode > 0) {
+        if (active) lds_fadd(bins + key, g);
+        return;
+    }
+    uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
+    const int h = key & (kCountSlots - 1);
+    if (active) __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    const uint32_t c = active ? lds_ld(cnt + h) : 0u;
+    if (active) lds_st(cnt + h, 0u);
+    const bool shared = active && c > 1;
+    if (shared) lds_fadd(bins + key, g);
+    if (active && c == 1) {
+        const T v = lds_ld(bins + key);
+        lds_st(bins + key, v + g);
+    }
+    if (mode < 0)
+        mode = __builtin_amdgcn_readfirstlane(__popcll(__ballot(shared)) > kAllSharedAbove ? 1 : 0);
 }
 
 // bins[key * es] += g in lane order among equal keys, bins in global memory
@@ -265,6 +267,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
         } else {
             bins_zero(bins, K);
         }
+        int mode = -1;
         // Contributions in chunks of PF blocks of 64 consecutive j.  The next
         // chunk's loads are issued before the current chunk is applied
         // (unconditional loads of clamped columns, so each wait covers only
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
                 if constexpr (GLOBAL)
                     global_apply<T>(bins, stage, 1, kc[u], gc[u], act[u], nbits);
                 else
-                    lds_apply<T>(bins, stage, kc[u], gc[u], act[u]);
+                    lds_apply<T>(bins, stage, kc[u], gc[u], act[u], mode);
             }
 #pragma unroll
             for (int u = 0; u < PF; ++u) {
@@ -391,6 +394,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                 bins_zero(bins, K);
             }
         }
+        int mode = -1;
         const int64_t cc = c0 + sq;
         const int64_t ccl = cc < N ? cc : N - 1;
         int32_t kr[TB];
@@ -429,7 +433,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                     if constexpr (GLOBAL)
                         global_apply<T>(bins, stage, es, key, g, active, nbits);
                     else
-                        lds_apply<T>(bins, stage, key, g, active);
+                        lds_apply<T>(bins, stage, key, g, active, mode);
                 }
             }
         }
