@@ -25,12 +25,14 @@
 //     consecutive ones.  So one atomic per contribution keeps the
 //     reference's order.  The LDS serves these atomics about one lane per
 //     2.6 clocks per CU, about 30x slower than integer adds, so a block first
-//     counts its lanes per hash of the bin (a per-wave table of kCountSlots
-//     integer counters: add, read back, clear), and only lanes whose hash
-//     is shared take the atomic; a lane alone with its hash (so alone with
-//     its bin) adds with a plain read and write.  A row (column) whose first
-//     block has more than kAllSharedAbove shared lanes is applied with
-//     atomics only: the count would not spare any.
+//     ranks its lanes per hash of the bin (a per-wave table of kCountSlots
+//     integer counters; an integer add with return, also served in lane
+//     order, gives each lane the number of earlier lanes with its hash).
+//     The first lane of each hash, which is the first lane of its bin, adds
+//     with a plain read and write and clears the counter; the later lanes
+//     then take the atomic.  A row (column) whose first block has more than
+//     kAllSharedAbove later lanes is applied with atomics only: the ranking
+//     would spare too few.
 //   * Bins in global memory (K too large for LDS: global_apply): the lanes
 //     sharing a bin are found by 64-bit ballots over the bits of the bin
 //     index (wave_match_mask), and the lowest lane of each group (its
@@ -174,7 +176,7 @@ __device__ __forceinline__ void bins_zero(T* bins, int64_t n) {
 }
 
 // LDS bins: counters per wave (in its stage, zero between blocks) and the
-// shared-lane count above which a row or column runs on atomics alone.
+// count of later lanes above which a row or column runs on atomics alone.
 constexpr int kCountSlots = 256;
 constexpr int kAllSharedAbove = 48;
 static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
@@ -182,7 +184,7 @@ static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
 
 // bins[key] += g in lane order among equal keys, bins in LDS (see the header
 // comment).  mode: -1 before a row's (column's) first block, which sets it
-// to 1 (atomics only) or 0 (count first).  Wave-uniform.
+// to 1 (atomics only) or 0 (rank first).  Wave-uniform.
 template <typename T>
 __device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active,
                                           int& mode) {
@@ -190,17 +192,23 @@ __device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, b
         if (active) lds_fadd(bins + key, g);
         return;
     }
+    // Integer adds with return are also served in lane order: r is the
+    // number of earlier lanes of the block with this hash.
     uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
     const int h = key & (kCountSlots - 1);
-    if (active) __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
-    const uint32_t c = active ? lds_ld(cnt + h) : 0u;
-    if (active) lds_st(cnt + h, 0u);
-    const bool shared = active && c > 1;
-    if (shared) lds_fadd(bins + key, g);
-    if (active && c == 1) {
+    const uint32_t r = active ? __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_WAVEFRONT)
+                              : 0u;
+    const bool first = active && r == 0;
+    const bool shared = active && r > 0;
+    if (first) {
         const T v = lds_ld(bins + key);
         lds_st(bins + key, v + g);
+        lds_st(cnt + h, 0u);
     }
+    // The firsts' writes are issued before the later lanes' adds.
+    asm volatile("" ::: "memory");
+    if (shared) lds_fadd(bins + key, g);
     if (mode < 0)
         mode = __builtin_amdgcn_readfirstlane(__popcll(__ballot(shared)) > kAllSharedAbove ? 1 : 0);
 }
