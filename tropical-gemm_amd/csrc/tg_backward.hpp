@@ -175,42 +175,54 @@ __device__ __forceinline__ void bins_zero(T* bins, int64_t n) {
     }
 }
 
-// LDS bins: counters per wave (in its stage, zero between blocks) and the
-// count of later lanes above which a row or column runs on atomics alone.
+// LDS bins: counters per wave (in its stage, zero between blocks), and the
+// counts of later lanes (lanes after the first of their hash in the block)
+// that set a row's (column's) mode from its first block.
 constexpr int kCountSlots = 256;
 constexpr int kAllSharedAbove = 48;
+constexpr int kSecondPlainAbove = 8;
 static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
               "the counters fit a wave's stage");
 
 // bins[key] += g in lane order among equal keys, bins in LDS (see the header
-// comment).  mode: -1 before a row's (column's) first block, which sets it
-// to 1 (atomics only) or 0 (rank first).  Wave-uniform.
-template <typename T>
-__device__ __forceinline__ void lds_apply(T* bins, T* stage, int32_t key, T g, bool active,
-                                          int& mode) {
-    if (mode > 0) {
+// comment), in one of three modes that a row (column) keeps from its first
+// block on.  MODE 0: the first lane of each hash adds plainly, the later
+// lanes take the ordered atomic.  MODE 2 (rows whose blocks repeat bins
+// often): the second lane of each hash also adds plainly, after the first,
+// so fewer lanes take the atomic.  MODE 1 (blocks of few bins): atomics
+// only.  Returns the mode that this block's ranks select.  Wave-uniform.
+template <int MODE, typename T>
+__device__ __forceinline__ int lds_apply(T* bins, uint32_t* cnt, int32_t key, T g, bool active) {
+    if constexpr (MODE == 1) {
         if (active) lds_fadd(bins + key, g);
-        return;
+        return 1;
+    } else {
+        // Integer adds with return are also served in lane order: r is the
+        // number of earlier lanes of the block with this hash.
+        const int h = key & (kCountSlots - 1);
+        const uint32_t r = active ? __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_WAVEFRONT)
+                                  : 0u;
+        if (active && r == 0) {
+            const T v = lds_ld(bins + key);
+            lds_st(bins + key, v + g);
+            lds_st(cnt + h, 0u);
+        }
+        // Each rank's writes are issued before the next rank's accesses.
+        asm volatile("" ::: "memory");
+        if constexpr (MODE == 2) {
+            if (active && r == 1) {
+                const T v = lds_ld(bins + key);
+                lds_st(bins + key, v + g);
+            }
+            asm volatile("" ::: "memory");
+        }
+        if (active && r >= (MODE == 2 ? 2u : 1u)) lds_fadd(bins + key, g);
+        const int later = __popcll(__ballot(active && r > 0));
+        return __builtin_amdgcn_readfirstlane(later > kAllSharedAbove      ? 1
+                                              : later > kSecondPlainAbove ? 2
+                                                                          : 0);
     }
-    // Integer adds with return are also served in lane order: r is the
-    // number of earlier lanes of the block with this hash.
-    uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
-    const int h = key & (kCountSlots - 1);
-    const uint32_t r = active ? __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_WAVEFRONT)
-                              : 0u;
-    const bool first = active && r == 0;
-    const bool shared = active && r > 0;
-    if (first) {
-        const T v = lds_ld(bins + key);
-        lds_st(bins + key, v + g);
-        lds_st(cnt + h, 0u);
-    }
-    // The firsts' writes are issued before the later lanes' adds.
-    asm volatile("" ::: "memory");
-    if (shared) lds_fadd(bins + key, g);
-    if (mode < 0)
-        mode = __builtin_amdgcn_readfirstlane(__popcll(__ballot(shared)) > kAllSharedAbove ? 1 : 0);
 }
 
 // bins[key * es] += g in lane order among equal keys, bins in global memory
@@ -259,6 +271,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
     constexpr int PF = 8;  // blocks of 64 contributions per prefetch chunk
     T* stage = reinterpret_cast<T*>(bwd_lds) + int64_t(wave) * kStageElems;
     T* row_bins = reinterpret_cast<T*>(bwd_lds) + int64_t(waves) * kStageElems + int64_t(wave) * K;
+    uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
     stage_clear(stage);
     for (int64_t rr = int64_t(blockIdx.x) * waves + wave; rr < rows;
          rr += int64_t(gridDim.x) * waves) {
@@ -300,13 +313,35 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
                 act[u] = j0 + 64 * u + lane < N && kc[u] >= 0 && int64_t(kc[u]) < K;
                 if (MULT && act[u]) gc[u] = gc[u] * other[int64_t(kc[u]) * N + j0 + 64 * u + lane];
             }
+            if constexpr (GLOBAL) {
 #pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                if (j0 + 64 * u >= N) break;
-                if constexpr (GLOBAL)
+                for (int u = 0; u < PF; ++u) {
+                    if (j0 + 64 * u >= N) break;
                     global_apply<T>(bins, stage, 1, kc[u], gc[u], act[u], nbits);
+                }
+            } else {
+                // The row's first block sets its mode; the mode's branch is
+                // taken once per chunk, so each mode's blocks are scheduled
+                // together.
+                int u0 = 0;
+                if (mode < 0) {
+                    mode = lds_apply<0, T>(bins, cnt, kc[0], gc[0], act[0]);
+                    u0 = 1;
+                }
+                auto blocks = [&](auto mc) __attribute__((always_inline)) {
+                    constexpr int MODE = decltype(mc)::value;
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        if (j0 + 64 * u >= N) break;
+                        if (u >= u0) lds_apply<MODE, T>(bins, cnt, kc[u], gc[u], act[u]);
+                    }
+                };
+                if (mode == 0)
+                    blocks(std::integral_constant<int, 0>{});
+                else if (mode == 2)
+                    blocks(std::integral_constant<int, 2>{});
                 else
-                    lds_apply<T>(bins, stage, kc[u], gc[u], act[u], mode);
+                    blocks(std::integral_constant<int, 1>{});
             }
 #pragma unroll
             for (int u = 0; u < PF; ++u) {
@@ -368,6 +403,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
     const int stride = W + 1;
     const int nbits = key_bits(K);
     T* stage = reinterpret_cast<T*>(bwd_lds) + wave * kStageElems;
+    uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
     unsigned char* const after_stage = bwd_lds + size_t(W) * kStageElems * sizeof(T);
     T* bins_all = reinterpret_cast<T*>(after_stage);
     const int64_t bins_bytes = GLOBAL ? 0 : int64_t(W) * K * int64_t(sizeof(T));
@@ -430,18 +466,48 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
             __syncthreads();
             stage_load(i0 + kBwdTileRows);
             if (c < N) {
-#pragma unroll
-                for (int t = 0; t < TB; ++t) {
+                // This column's blocks of the tile, in row order.
+                auto block = [&](int t, int32_t& key, T& g, bool& active) __attribute__((always_inline)) {
                     const int64_t it = i0 + 64 * t;
-                    if (it >= M) break;
-                    const int32_t key = tile_k[(64 * t + lane) * stride + wave];
-                    T g = tile_g[(64 * t + lane) * stride + wave];
-                    const bool active = key >= 0 && int64_t(key) < K;
+                    key = tile_k[(64 * t + lane) * stride + wave];
+                    g = tile_g[(64 * t + lane) * stride + wave];
+                    active = it < M && key >= 0 && int64_t(key) < K;
                     if (MULT && active) g = g * other[(it + lane) * K + key];
-                    if constexpr (GLOBAL)
+                };
+                if constexpr (GLOBAL) {
+#pragma unroll
+                    for (int t = 0; t < TB; ++t) {
+                        if (i0 + 64 * t >= M) break;
+                        int32_t key; T g; bool active;
+                        block(t, key, g, active);
                         global_apply<T>(bins, stage, es, key, g, active, nbits);
+                    }
+                } else {
+                    int t0 = 0;
+                    if (mode < 0) {
+                        int32_t key; T g; bool active;
+                        block(0, key, g, active);
+                        mode = lds_apply<0, T>(bins, cnt, key, g, active);
+                        t0 = 1;
+                    }
+                    auto blocks = [&](auto mc) __attribute__((always_inline)) {
+                        constexpr int MODE = decltype(mc)::value;
+#pragma unroll
+                        for (int t = 0; t < TB; ++t) {
+                            if (i0 + 64 * t >= M) break;
+                            if (t >= t0) {
+                                int32_t key; T g; bool active;
+                                block(t, key, g, active);
+                                lds_apply<MODE, T>(bins, cnt, key, g, active);
+                            }
+                        }
+                    };
+                    if (mode == 0)
+                        blocks(std::integral_constant<int, 0>{});
+                    else if (mode == 2)
+                        blocks(std::integral_constant<int, 2>{});
                     else
-                        lds_apply<T>(bins, stage, key, g, active, mode);
+                        blocks(std::integral_constant<int, 1>{});
                 }
             }
         }
