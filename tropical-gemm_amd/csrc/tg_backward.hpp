@@ -94,9 +94,10 @@ __device__ __forceinline__ void lds_fadd(T* p, T v) {
 
 // Ranks per stage pass.  A wave's stage: 64 leaders x kStageRanks slots
 // (with LDS bins: the block's counters instead).  Passes per wait
-// (group_sum): 2 took C5-like argmax (MaxPlus f32 4096^3) from 129 to 122 us
-// for grad_A and 158 to 148 us for grad_B against 1 pass; 4 was slower on
-// uniformly random indices.
+// (group_sum, which the global-bin kernels use): measured when the LDS-bin
+// kernels summed their groups the same way, 2 took C5-like argmax (MaxPlus
+// f32 4096^3) from 129 to 122 us for grad_A and 158 to 148 us for grad_B
+// against 1 pass; 4 was slower on uniformly random indices.
 constexpr int kStageRanks = 4;
 constexpr int kStagePasses = 2;
 constexpr int kStageSlots = kStageRanks * 64;
