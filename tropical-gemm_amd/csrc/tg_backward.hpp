@@ -30,9 +30,12 @@
 //     order, gives each lane the number of earlier lanes with its hash).
 //     The first lane of each hash, which is the first lane of its bin, adds
 //     with a plain read and write and clears the counter; the later lanes
-//     then take the atomic.  A row (column) whose first block has more than
-//     kAllSharedAbove later lanes is applied with atomics only: the ranking
-//     would spare too few.
+//     then take the atomic.  A row (column) keeps a mode from its first
+//     block: with more than kSecondPlainAbove later lanes there, the second
+//     lane of each hash also adds plainly (after the first), and with more
+//     than kAllSharedAbove the row runs on atomics only (the ranking would
+//     spare too few).  The mode's branch is taken once per group of blocks,
+//     so each mode's blocks are scheduled without per-block branches.
 //   * Bins in global memory (K too large for LDS: global_apply): the lanes
 //     sharing a bin are found by 64-bit ballots over the bits of the bin
 //     index (wave_match_mask), and the lowest lane of each group (its
