@@ -25,9 +25,10 @@
 //     consecutive ones.  So one atomic per contribution keeps the
 //     reference's order.  The LDS serves these atomics about one lane per
 //     2.6 clocks per CU, about 30x slower than integer adds, so a block first
-//     ranks its lanes per hash of the bin (a per-wave table of kCountSlots
-//     integer counters; an integer add with return, also served in lane
-//     order, gives each lane the number of earlier lanes with its hash).
+//     ranks its lanes per hash of the bin (a per-wave table of integer
+//     counters, kRowCountSlots for grad_A and kCountSlots for grad_B; an
+//     integer add with return, also served in lane order, gives each lane
+//     the number of earlier lanes with its hash).
 //     The first lane of each hash, which is the first lane of its bin, adds
 //     with a plain read and write and clears the counter; the later lanes
 //     then take the atomic.  A row (column) keeps a mode from its first
@@ -113,6 +114,10 @@ constexpr int kStageRanks = 4;
 constexpr int kStagePasses = 2;
 constexpr int kStageSlots = kStageRanks * 64;
 constexpr int kStageElems = kStageSlots;
+// grad_A's stage is twice as large: its LDS-bin rows rank on 512 counters
+// (fewer hash collisions, so fewer lanes take the atomic), and one row more
+// or less per CU changes nothing at K = 4096 (eight instead of nine).
+constexpr int kRowStageElems = 2 * kStageSlots;
 
 // The leader's sum before + g(leader) + g(rank 1) + g(rank 2) + ... of its
 // group (m: this lane's group mask, 0 when inactive); meaningful on leaders
@@ -162,13 +167,13 @@ __device__ __forceinline__ T group_sum(uint64_t m, T g, T before, bool& leader, 
     return acc;
 }
 
-// Zeroes the slots of this wave's stage (which holds at least kCountSlots
-// 32-bit counters).
-template <typename T>
+// Zeroes this wave's stage of ELEMS elements (which hold its 32-bit
+// counters with LDS bins).
+template <int ELEMS, typename T>
 __device__ __forceinline__ void stage_clear(T* stage) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int u = 0; u < kStageRanks; ++u) stage[u * 64 + lane] = T(0);
+    for (int u = 0; u < ELEMS / 64; ++u) stage[u * 64 + lane] = T(0);
     asm volatile("" ::: "memory");
 }
 
@@ -190,10 +195,12 @@ __device__ __forceinline__ void bins_zero(T* bins, int64_t n) {
 // LDS bins: counters per wave (in its stage, zero between blocks), and the
 // counts of later lanes (lanes after the first of their hash in the block)
 // that set a row's (column's) mode from its first block.
-constexpr int kCountSlots = 256;
+constexpr int kCountSlots = 256;     // grad_B (its stage)
+constexpr int kRowCountSlots = 512;  // grad_A (its larger stage)
 constexpr int kAllSharedAbove = 48;
 constexpr int kSecondPlainAbove = 8;
-static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
+static_assert(kCountSlots * sizeof(uint32_t) <= kStageElems * sizeof(float) &&
+                  kRowCountSlots * sizeof(uint32_t) <= kRowStageElems * sizeof(float),
               "the counters fit a wave's stage");
 
 // bins[key] += g in lane order among equal keys, bins in LDS (see the header
@@ -203,7 +210,7 @@ static_assert(kCountSlots * sizeof(uint32_t) <= kStageSlots * sizeof(float),
 // often): the second lane of each hash also adds plainly, after the first,
 // so fewer lanes take the atomic.  MODE 1 (blocks of few bins): atomics
 // only.  Returns the mode that this block's ranks select.  Wave-uniform.
-template <int MODE, typename T>
+template <int MODE, int SLOTS, typename T>
 __device__ __forceinline__ int lds_apply(T* bins, uint32_t* cnt, int32_t key, T g, bool active) {
     if constexpr (MODE == 1) {
         if (active) lds_fadd(bins + key, g);
@@ -211,7 +218,7 @@ __device__ __forceinline__ int lds_apply(T* bins, uint32_t* cnt, int32_t key, T 
     } else {
         // Integer adds with return are also served in lane order: r is the
         // number of earlier lanes of the block with this hash.
-        const int h = key & (kCountSlots - 1);
+        const int h = key & (SLOTS - 1);
         const uint32_t r = active ? __hip_atomic_fetch_add(cnt + h, 1u, __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_WAVEFRONT)
                                   : 0u;
@@ -263,8 +270,8 @@ __device__ __forceinline__ void global_apply(T* bins, T* stage, int64_t es, int3
 
 // ---------------------------------------------------------------------------
 // grad_A.  rows = batch * M; row rr is (z = rr / M, i = rr % M).  Each wave
-// owns one row at a time; LDS: a stage of kStageElems per wave, then K bins
-// per wave (not with GLOBAL): waves * (kStageElems + K) * sizeof(T).
+// owns one row at a time; LDS: a stage of kRowStageElems per wave, then K
+// bins per wave (not with GLOBAL): waves * (kRowStageElems + K) * sizeof(T).
 //   MULT: MaxMul rule, g *= B[z][k][j] (OTHER = B, row-major K x N).
 // GLOBAL: the bins are the grad_A row itself (K too large for LDS).
 // grid: any size (grid-stride over rows), block = 64 * waves.
@@ -281,10 +288,11 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
     const int waves = blockDim.x >> 6;
     const int nbits = key_bits(K);
     constexpr int PF = 8;  // blocks of 64 contributions per prefetch chunk
-    T* stage = reinterpret_cast<T*>(bwd_lds) + int64_t(wave) * kStageElems;
-    T* row_bins = reinterpret_cast<T*>(bwd_lds) + int64_t(waves) * kStageElems + int64_t(wave) * K;
+    T* stage = reinterpret_cast<T*>(bwd_lds) + int64_t(wave) * kRowStageElems;
+    T* row_bins =
+        reinterpret_cast<T*>(bwd_lds) + int64_t(waves) * kRowStageElems + int64_t(wave) * K;
     uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
-    stage_clear(stage);
+    stage_clear<kRowStageElems>(stage);
     for (int64_t rr = int64_t(blockIdx.x) * waves + wave; rr < rows;
          rr += int64_t(gridDim.x) * waves) {
         const int64_t z = rr / M, i = rr - z * M;
@@ -337,7 +345,7 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
                 // together.
                 int u0 = 0;
                 if (mode < 0) {
-                    mode = lds_apply<0, T>(bins, cnt, kc[0], gc[0], act[0]);
+                    mode = lds_apply<0, kRowCountSlots, T>(bins, cnt, kc[0], gc[0], act[0]);
                     u0 = 1;
                 }
                 auto blocks = [&](auto mc) __attribute__((always_inline)) {
@@ -345,7 +353,8 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
 #pragma unroll
                     for (int u = 0; u < PF; ++u) {
                         if (j0 + 64 * u >= N) break;
-                        if (u >= u0) lds_apply<MODE, T>(bins, cnt, kc[u], gc[u], act[u]);
+                        if (u >= u0)
+                            lds_apply<MODE, kRowCountSlots, T>(bins, cnt, kc[u], gc[u], act[u]);
                     }
                 };
                 if (mode == 0)
@@ -422,7 +431,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
     T* tile_g = reinterpret_cast<T*>(after_stage + bins_bytes);
     int32_t* tile_k =
         reinterpret_cast<int32_t*>(after_stage + bins_bytes + kBwdTileRows * stride * sizeof(T));
-    stage_clear(stage);
+    stage_clear<kStageElems>(stage);
     // This thread's staging slots: rows sr + 64 t (t < TB), column sq.
     const int sr = tid / W, sq = tid - (tid / W) * W;
     // XCD-aware order: with a grid that is a multiple of 8, launch slot b
@@ -499,7 +508,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                     if (mode < 0) {
                         int32_t key; T g; bool active;
                         block(0, key, g, active);
-                        mode = lds_apply<0, T>(bins, cnt, key, g, active);
+                        mode = lds_apply<0, kCountSlots, T>(bins, cnt, key, g, active);
                         t0 = 1;
                     }
                     auto blocks = [&](auto mc) __attribute__((always_inline)) {
@@ -510,7 +519,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                             if (t >= t0) {
                                 int32_t key; T g; bool active;
                                 block(t, key, g, active);
-                                lds_apply<MODE, T>(bins, cnt, key, g, active);
+                                lds_apply<MODE, kCountSlots, T>(bins, cnt, key, g, active);
                             }
                         }
                     };

@@ -1231,13 +1231,13 @@ struct BwdGeometry {
 };
 
 // grad_A: one wave per row; a wave's LDS is its row's K bins plus its stage
-// (tg::kStageElems elements).  Four waves per workgroup while that is at
-// most 8 KB, two while at most 16 KB, else one (17 KB at K = 4096 f32: nine
+// (tg::kRowStageElems elements).  Four waves per workgroup while that is at
+// most 8 KB, two while at most 16 KB, else one (18 KB at K = 4096 f32: eight
 // workgroups per CU); global bins beyond the LDS budget.
 BwdGeometry bwd_rows_geometry(int64_t rows, int64_t K, size_t es) {
     BwdGeometry g;
     const size_t row_bytes = size_t(K) * es;
-    const size_t stage_bytes = size_t(tg::kStageElems) * es;
+    const size_t stage_bytes = size_t(tg::kRowStageElems) * es;
     const size_t wave_bytes = row_bytes + stage_bytes;
     if (row_bytes > kBwdLdsBudget) {
         g.global = true;
