@@ -244,12 +244,27 @@ __device__ __forceinline__ int lds_apply(T* bins, uint32_t* cnt, int32_t key, T 
     }
 }
 
-// bins[key * es] += g in lane order among equal keys, bins in global memory
-// (read and written by the leaders with relaxed device-scope atomics).  The
-// next block's leader for a bin may be another lane, so the trailing
-// device-scope fence waits until this block's writes have reached L2 before
-// the wave issues its next reads (a workgroup-scope fence does not wait for
-// them).  Wave-uniform.
+// Global bins belong to one wave and only its own lanes read them back, so
+// their accesses are workgroup-scope atomics ordered by a workgroup-scope
+// fence.  The lanes of a wave go through one CU's vector memory pipeline and
+// L1 in order, so the AMDGPU memory model needs no wait or cache action for
+// coherence among them (the fence compiles to none outside tgsplit mode).  A
+// device-scope fence would also write the XCD's L2 back to memory
+// (buffer_wbl2 on gfx950) on every block, for other XCDs these bins never
+// reach.
+template <typename T>
+__device__ __forceinline__ T gbin_ld(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <typename T>
+__device__ __forceinline__ void gbin_st(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void gbin_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup"); }
+
+// bins[key * es] += g in lane order among equal keys, bins in global memory.
+// The next block's leader for a bin may be another lane, so this block's
+// writes are fenced before the wave issues its next reads.  Wave-uniform.
 template <typename T>
 __device__ __forceinline__ void global_apply(T* bins, T* stage, int64_t es, int32_t key, T g,
                                              bool active, int nbits) {
@@ -257,15 +272,11 @@ __device__ __forceinline__ void global_apply(T* bins, T* stage, int64_t es, int3
     const int lane = threadIdx.x & 63;
     const bool first = m != 0 && int(__builtin_ctzll(m)) == lane;
     T before = T(0);
-    if (first)
-        before = __hip_atomic_load(bins + int64_t(key) * es, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+    if (first) before = gbin_ld(bins + int64_t(key) * es);
     bool leader;
     const T acc = group_sum(m, g, before, leader, stage);
-    if (leader)
-        __hip_atomic_store(bins + int64_t(key) * es, acc, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    __threadfence();
+    if (leader) gbin_st(bins + int64_t(key) * es, acc);
+    gbin_fence();
 }
 
 // ---------------------------------------------------------------------------
@@ -302,9 +313,8 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
         T* out = GA + z * sA + i * K;
         T* bins = GLOBAL ? out : row_bins;
         if constexpr (GLOBAL) {
-            for (int64_t k = lane; k < K; k += 64)
-                __hip_atomic_store(bins + k, T(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence();  // zeros visible to every lane's first read
+            for (int64_t k = lane; k < K; k += 64) gbin_st(bins + k, T(0));
+            gbin_fence();  // zeros visible to every lane's first read
         } else {
             bins_zero(bins, K);
         }
@@ -451,10 +461,8 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
         const int64_t es = GLOBAL ? N : 1;
         if (c < N) {
             if constexpr (GLOBAL) {
-                for (int64_t k = lane; k < K; k += 64)
-                    __hip_atomic_store(bins + k * es, T(0), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                __threadfence();
+                for (int64_t k = lane; k < K; k += 64) gbin_st(bins + k * es, T(0));
+                gbin_fence();
             } else {
                 bins_zero(bins, K);
             }
