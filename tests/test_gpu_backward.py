@@ -386,6 +386,36 @@ def test_backward_bins_in_global_memory(dtype, k):
     assert_bits(ops.backward_b(tg_, tam, k).cpu().numpy(), oracle.backward_b(g, am.astype(np.uint32), k))
 
 
+@pytest.mark.parametrize("mult", [False, True])
+@pytest.mark.parametrize("dtype,k,waves", [(np.float32, 8192, 4), (np.float32, 12000, 3),
+                                           (np.float32, 16384, 2), (np.float32, 32768, 1),
+                                           (np.float64, 4096, 4), (np.float64, 16384, 1)])
+def test_backward_cols_long_columns_in_lds(dtype, k, waves, mult):
+    """grad_B with long columns whose bins still fit the LDS, fewer than eight
+    per workgroup: a column group that ends past N, rows that end inside a
+    tile, bins repeated within blocks, out-of-range indices, and the
+    column-by-column write-out must still give the reference's bits."""
+    from tropical_gemm import _native as nat, ops
+
+    m, n = 300, 21
+    dt = 0 if dtype == np.float32 else 1
+    plan = nat.load().tg_backward_plan(dt, 0, 0, 1, m, n, k).decode()
+    print(f"[case] grad_B long columns {np.dtype(dtype).name} k={k} mult={mult}: {plan}", flush=True)
+    assert plan.startswith("cols lds") and f"waves={waves} " in plan, plan
+    rng = np.random.default_rng(k + waves)
+    g = rng.standard_normal((m, n)).astype(dtype)
+    am = rng.integers(0, k, size=(m, n))
+    am[:96] = rng.choice([0, 1, k // 2, k - 2, k - 1], size=(96, n))  # few bins, repeated within blocks
+    am[200:264, ::3] = k // 3  # one bin for a whole block
+    am[5, 2], am[70, 4], am[299, 20] = -1, k, k + 5  # skipped
+    a = rng.standard_normal((m, k)).astype(dtype) if mult else None
+    tg_, tam = torch.from_numpy(g).to(DEV), torch.from_numpy(am.astype(np.int32)).to(DEV)
+    ta = torch.from_numpy(a).to(DEV) if mult else None
+    gb = ops.backward_b(tg_, tam, k, a=ta).cpu().numpy()
+    ref = oracle.backward_b(g, np.where(am < 0, 1 << 30, am).astype(np.uint32), k, a)
+    assert_bits(gb, ref)
+
+
 @pytest.mark.parametrize("name", ["maxplus", "minplus", "maxmul"])
 def test_autograd_batched_classes(name):
     from tropical_gemm import pytorch as tp
