@@ -77,7 +77,7 @@ KERNEL_NAMES = {
     "M1": "tg_gemm_shortk<MaxPlus, f32, argmax> (32x256 tiles, per-product index)",
     "F1": "tg_gemm_dl64<MaxPlus> (f64, 64x128 tiles, argmax)",
     "F2": "tg_gemm_dl64<MaxPlus, value-only> (f64, 64x128 tiles)",
-    "I1": "tg_gemm_tiles<MaxPlus, i64, chunked argmax> (64x64 tiles)",
+    "I1": "tg_gemm_tiles<MaxPlus, i64, chunked argmax, 16-k chunks> (64x64 tiles)",
     "I2": "tg_gemm_tiles<MaxPlus, i64, value-only> (64x64 tiles)",
 }
 # HBM bytes per launch of the dominant kernel from rocprofv3 --pmc FETCH_SIZE
@@ -89,7 +89,7 @@ KERNEL_NAMES = {
 
 TRAFFIC = {"P": 1.924e9, "C5": 1.924e9, "C4": 0.418e9, "M1": 1.108e9, "C1": 0.034e9,
            "C2": 1.771e9, "C3": 0.704e9, "F1": 3.439e9, "F2": 2.266e9, "E1": 0.1177e9,
-           "I1": 7.997e9, "I2": 3.356e9}
+           "I1": 4.881e9, "I2": 3.356e9}
 
 
 def cpu_model() -> str:

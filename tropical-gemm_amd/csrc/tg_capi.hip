@@ -945,15 +945,19 @@ int run_gemm_typed(const Problem& p, void* ws, size_t ws_bytes, hipStream_t st) 
                 const int rc = launch_transpose<T>(Bz, BT, p.K, p.N, p.sB, sBT, nb, st);
                 if (rc != TG_OK) return rc;
             }
+            // 64-bit integers record 16-k chunks: their 128-byte windows halve
+            // what the resolve reads (it misses L2), for one record per 64
+            // instructions of products instead of 128.
+            constexpr int CL = std::is_same<T, int64_t>::value ? 16 : tg::TG_CHUNK;
             KernelTimer timer(st);
             if (vec)
-                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true>), grid, dim3(256), 0, st,
-                                   Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, true, false, CL>), grid, dim3(256),
+                                   0, st, Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
                                    int(tiles_m), int(tiles_n));
             else
-                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false>), grid, dim3(256), 0, st,
-                                   Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB, p.sC,
-                                   int(tiles_m), int(tiles_n));
+                hipLaunchKernelGGL((tg::tg_gemm_tiles<SR, T, true, false, false, CL>), grid,
+                                   dim3(256), 0, st, Az, Bz, BT, Cz, Iz, p.M, p.N, p.K, p.sA, p.sB,
+                                   p.sC, int(tiles_m), int(tiles_n));
             TG_HIP(hipGetLastError());
         } else {
             KernelTimer timer(st);

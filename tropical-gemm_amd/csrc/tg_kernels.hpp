@@ -13,26 +13,27 @@
 // onto row-major ones with the operand swap C^T = B^T (x) A^T
 // (kernels.rs:370-430 does the same trick in the other direction).
 //
-// Argmax scheme ("chunked argmax").  K is cut into chunks of TG_CHUNK = 32
-// consecutive k (one LDS k-tile).  Inside a chunk each output folds its
+// Argmax scheme ("chunked argmax").  K is cut into chunks of CL consecutive k
+// (TG_CHUNK = 32, one LDS k-tile, or an even part of it: 16 for 64-bit
+// integers).  Inside a chunk each output folds its
 // products into a chunk maximum with max/min only (two products per
 // v_max3/v_min3).  At the chunk end one compare against the running value
 // records the chunk index if the chunk strictly improved it.  Because max/min
 // select an operand exactly and earlier chunks only lose on strict
 // improvement, the first k attaining the final value lies in the recorded
-// chunk; the kernel's epilogue finds it by recomputing that chunk's <= 32
+// chunk; the kernel's epilogue finds it by recomputing that chunk's <= CL
 // products (reading A and B^T rows) and takes the first k whose product
 // equals the final value, writing both the index and that product's bits (so
 // a -0/+0 tie keeps the first occurrence's sign, exactly like the CPU select
-// rule).  The per-(i,j,k) VALU cost is one (x), half a max3 and 3/32 for the
-// bookkeeping instead of the four operations of a per-k compare-and-select.
+// rule).  The per-(i,j,k) VALU cost is one (x), half a max3 and 2/CL for the
+// records instead of the four operations of a per-k compare-and-select.
 #pragma once
 
 #include "tg_device.hpp"
 
 namespace tg {
 
-constexpr int TG_CHUNK = 32;   // k per LDS tile == argmax chunk length
+constexpr int TG_CHUNK = 32;   // k per LDS tile == the default argmax chunk length
 constexpr int TG_THREADS = 256;
 
 // Tile shapes.  4-byte types: 128 x 64 output tile, 8 x 4 outputs per thread.
@@ -86,11 +87,14 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 // Main GEMM kernel.
 //   ARGMAX=false : C = A (x) B.
 //   ARGMAX=true  : C = A (x) B and IDX = the first k attaining C.  The main
-//                  loop folds each chunk of TG_CHUNK consecutive k into a
-//                  chunk maximum cm and records the chunk when cm strictly
-//                  beats the running value; the epilogue then re-reads that
+//                  loop folds each chunk of CL consecutive k into a chunk
+//                  maximum cm and records the chunk when cm strictly beats
+//                  the running value; the epilogue then re-reads that
 //                  chunk's A-row and B^T-row segments (BT from tg_transpose)
 //                  and takes the first k whose product equals the final value.
+//   CL           : argmax chunk length, TG_CHUNK / SUB.  Shorter chunks cost
+//                  more records and shorten the windows the resolve reads
+//                  (which miss L2): 64-bit integers use 16.
 //   VEC          : K and N are multiples of 16/sizeof(T) and A, B, BT are
 //                  16-byte aligned, so tiles and argmax windows use 16-byte
 //                  global loads.
@@ -100,7 +104,7 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 //                  re-reads of A and B^T would outweigh the main loop.
 // grid = (tiles_m * tiles_n, 1, batch), block = 256.
 // ---------------------------------------------------------------------------
-template <int SR, typename T, bool ARGMAX, bool VEC, bool EXACT = false>
+template <int SR, typename T, bool ARGMAX, bool VEC, bool EXACT = false, int CL = TG_CHUNK>
 __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ BT,
     T* __restrict__ C, int32_t* __restrict__ IDX, int64_t M, int64_t N, int64_t K, int64_t sA,
@@ -114,6 +118,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     static_assert(NVA >= 1 && NVB >= 1, "tile too small for the block");
     static_assert(TM % 4 == 0 && TN % 4 == 0, "micro-tile must be made of 4-wide groups");
     static_assert(ARGMAX || !EXACT, "EXACT is an argmax mode");
+    static_assert(BK % CL == 0 && CL % 8 == 0, "argmax chunks split the k-tile evenly");
+    constexpr int SUB = BK / CL;  // argmax chunks per k-tile
 
     __shared__ __align__(16) T As[2][BK][BM + PAD];
     __shared__ __align__(16) T Bs[2][BK][BN + PAD];
@@ -312,61 +318,71 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
             __syncthreads();
             continue;
         }
-        // Chunk maximum (minimum for MinPlus) over this chunk's products.
-        T cm[TM][TN];
-        if (k0 + BK <= K) {
-            T a0[TM], b0[TN], a1[TM], b1[TN];
-            load_frag(buf, 0, a0, b0);
-            load_frag(buf, 1, a1, b1);
+        // Chunk maximum (minimum for MinPlus) over each chunk's products, then
+        // its record.  Strict improvement only: an equal chunk maximum keeps
+        // the earlier chunk, which is the reference's "keep acc iff acc >= p"
+        // rule.
+        auto fold = [&](T (&cm)[TM][TN], int32_t chunk) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a0[i], b0[j]), tmul<SR, T>(a1[i], b1[j]));
-            // Remaining products two at a time: one max3/min3 per pair.
-#pragma unroll
-            for (int kk = 2; kk < BK; kk += 2) {
-                load_frag(buf, kk, a0, b0);
-                load_frag(buf, kk + 1, a1, b1);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        const T p0 = tmul<SR, T>(a0[i], b0[j]);
-                        const T p1 = tmul<SR, T>(a1[i], b1[j]);
-                        cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
+                for (int j = 0; j < TN; ++j) {
+                    if constexpr (ARGMAX) {
+                        if (tbetter<SR, T>(cm[i][j], acc[i][j])) ch[i][j] = chunk;
                     }
-            }
-        } else {
-            // Ragged last chunk: only k < K may enter the reduction.
-            const int kcnt = int(K - k0);
-            T a0[TM], b0[TN];
-            load_frag(buf, 0, a0, b0);
+                    acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
+                }
+        };
+        const bool full = k0 + BK <= K;
+        const int kcnt = full ? BK : int(K - k0);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) cm[i][j] = tmul<SR, T>(a0[i], b0[j]);
-            for (int kk = 1; kk < kcnt; ++kk) {
-                load_frag(buf, kk, a0, b0);
+        for (int s = 0; s < SUB; ++s) {
+            const int kb = s * CL;
+            if (kb >= kcnt) break;
+            T cm[TM][TN];
+            if (full) {
+                T a0[TM], b0[TN], a1[TM], b1[TN];
+                load_frag(buf, kb, a0, b0);
+                load_frag(buf, kb + 1, a1, b1);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        cm[i][j] = tjoin<SR, T>(cm[i][j], tmul<SR, T>(a0[i], b0[j]));
-            }
-        }
-
-        // Strict improvement only: an equal chunk maximum keeps the earlier
-        // chunk, which is the reference's "keep acc iff acc >= p" rule.
+                        cm[i][j] = tjoin<SR, T>(tmul<SR, T>(a0[i], b0[j]), tmul<SR, T>(a1[i], b1[j]));
+                // Remaining products two at a time: one max3/min3 per pair.
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+                for (int kk = kb + 2; kk < kb + CL; kk += 2) {
+                    load_frag(buf, kk, a0, b0);
+                    load_frag(buf, kk + 1, a1, b1);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                if constexpr (ARGMAX) {
-                    if (tbetter<SR, T>(cm[i][j], acc[i][j])) ch[i][j] = int32_t(t);
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
+                            const T p0 = tmul<SR, T>(a0[i], b0[j]);
+                            const T p1 = tmul<SR, T>(a1[i], b1[j]);
+                            cm[i][j] = tjoin<SR, T>(tjoin<SR, T>(cm[i][j], p0), p1);
+                        }
                 }
-                acc[i][j] = tjoin<SR, T>(acc[i][j], cm[i][j]);
+            } else {
+                // Ragged last k-tile: only k < K may enter the reduction.
+                const int ke = kb + CL < kcnt ? kb + CL : kcnt;
+                T a0[TM], b0[TN];
+                load_frag(buf, kb, a0, b0);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) cm[i][j] = tmul<SR, T>(a0[i], b0[j]);
+                for (int kk = kb + 1; kk < ke; ++kk) {
+                    load_frag(buf, kk, a0, b0);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            cm[i][j] = tjoin<SR, T>(cm[i][j], tmul<SR, T>(a0[i], b0[j]));
+                }
             }
+            fold(cm, int32_t(t * SUB + s));
+        }
 
         if (t + 1 < ntiles) store_tiles(buf ^ 1);
         __syncthreads();
@@ -462,13 +478,15 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
     } else {
         // Exact argmax inside the recorded chunk.  Products in the chunk
         // before it never equal the final value (that chunk would not have
-        // been beaten strictly), so a 16-byte-aligned window of TG_CHUNK
-        // products ending at K may be searched for the ragged last chunk.
-        // The value written is the bits of the first equal product, so a
-        // -0/+0 tie keeps the first occurrence's sign like the CPU rule.
-        constexpr int NW = BK / VW;                // 16-byte vectors per window
-        constexpr int G = sizeof(T) == 4 ? 2 : 1;  // outputs with windows in flight
-        const bool vec_windows = VEC && K >= BK;
+        // been beaten strictly), so a 16-byte-aligned window of CL products
+        // ending at K may be searched for the ragged last chunk.  The value
+        // written is the bits of the first equal product, so a -0/+0 tie
+        // keeps the first occurrence's sign like the CPU rule.
+        constexpr int NW = CL / VW;  // 16-byte vectors per window
+        // Outputs with windows in flight: two while a window is one 128-byte
+        // line per operand.
+        constexpr int G = CL * int(sizeof(T)) <= 128 ? 2 : 1;
+        const bool vec_windows = VEC && K >= CL;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int64_t gr = row0 + (i / 4) * 64 + ty * 4 + (i % 4);
@@ -493,7 +511,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                     for (int g = 0; g < G; ++g) {
                         const int64_t gcl = gc[g] < N ? gc[g] : N - 1;
                         const int64_t c = ch[i][j0 + g] < 0 ? 0 : ch[i][j0 + g];
-                        ws[g] = (c * BK < K - BK) ? c * BK : K - BK;
+                        ws[g] = (c * CL < K - CL) ? c * CL : K - CL;
                         ap[g] = A + grl * K + ws[g];
                         bp[g] = BT + gcl * K + ws[g];
 #pragma unroll
@@ -509,7 +527,7 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                         // of 8 compares keep few lane masks live at once.
                         int32_t f = 0;
 #pragma unroll
-                        for (int q = BK / 8 - 1; q >= 0; --q) {
+                        for (int q = CL / 8 - 1; q >= 0; --q) {
 #pragma unroll
                             for (int kk = q * 8 + 7; kk >= q * 8; --kk) {
                                 const T p = tmul<SR, T>(av[g][kk / VW].v[kk % VW],
@@ -531,8 +549,8 @@ __global__ __launch_bounds__(TG_THREADS) void tg_gemm_tiles(
                         const int32_t c = ch[i][j0 + g];
                         if (gr < M && gc[g] < N && c >= 0) {
                             const T target = val[g];
-                            const int64_t k0 = int64_t(c) * BK;
-                            const int64_t k1 = (k0 + BK < K) ? k0 + BK : K;
+                            const int64_t k0 = int64_t(c) * CL;
+                            const int64_t k1 = (k0 + CL < K) ? k0 + CL : K;
                             idx[g] = int32_t(k0);
                             for (int64_t k = k0; k < k1; ++k) {
                                 const T p = tmul<SR, T>(A[gr * K + k], BT[gc[g] * K + k]);
