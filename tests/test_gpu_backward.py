@@ -386,6 +386,41 @@ def test_backward_bins_in_global_memory(dtype, k):
     assert_bits(ops.backward_b(tg_, tam, k).cpu().numpy(), oracle.backward_b(g, am.astype(np.uint32), k))
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("gap", [0, 1000])
+def test_backward_b_global_bins_batched(dtype, gap):
+    """grad_B with its bins in global memory on a strided batch, dense
+    (gap 0) or with `gap` elements between the items: the gradient is
+    zero-filled item by item before the scatter, and the gaps keep their
+    bytes."""
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    batch, m, n, k = 3, 7, 130, 40000
+    dt = 0 if dtype == np.float32 else 1
+    plan = lib.tg_backward_plan(dt, 0, 0, batch, m, n, k).decode()
+    print(f"[case] grad_B global bins batched {np.dtype(dtype).name} gap={gap}: {plan}", flush=True)
+    assert plan.startswith("cols global"), plan
+    rng = np.random.default_rng(4000 + gap)
+    g = rng.standard_normal((batch, m, n)).astype(dtype)
+    am = rng.integers(0, k, size=(batch, m, n))
+    am[:, :, :40] = 5  # one bin repeated within blocks
+    am[0, 0, 0], am[1, 2, 3] = -1, k  # skipped
+    s_b = k * n + gap
+    out = torch.full((batch * s_b,), 7.0, dtype=torch.float32 if dt == 0 else torch.float64, device=DEV)
+    tg_ = torch.from_numpy(g).to(DEV)
+    tam = torch.from_numpy(am.astype(np.int32)).to(DEV)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    nat.check(lib.tg_backward_b_strided_batched(0, dt, 0, p(tg_), p(tam), None, p(out), batch, m, n, k,
+                                                m * n, 0, s_b, None))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for t in range(batch):
+        ref = oracle.backward_b(g[t], np.where(am[t] < 0, 1 << 30, am[t]).astype(np.uint32), k)
+        assert_bits(got[t * s_b:t * s_b + k * n].reshape(k, n), ref)
+        assert (got[t * s_b + k * n:(t + 1) * s_b] == 7.0).all()
+
+
 @pytest.mark.parametrize("mult", [False, True])
 @pytest.mark.parametrize("dtype,k,waves", [(np.float32, 8192, 4), (np.float32, 12000, 3),
                                            (np.float32, 16384, 2), (np.float32, 32768, 1),

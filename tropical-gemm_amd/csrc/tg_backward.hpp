@@ -413,6 +413,9 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
 // column groups, so the W-column segments that share a cache line are read
 // and written through one L2.
 //   MULT: MaxMul rule, g *= A[z][i][k] (OTHER = A, row-major M x K).
+// GLOBAL: the bins are the grad_B column itself, which the host zero-fills
+// before the launch (one coalesced pass: zeroing a column here would take
+// K stores of 4 or 8 bytes, N elements apart).
 // LDS: a stage of kStageElems per wave, W * K bins (not with GLOBAL), then
 // the tile, kBwdTileRows (W + 1) (4 + sizeof(T)) bytes.
 // grid: any size (grid-stride over column groups), block = 64 * W, W <= 8.
@@ -459,14 +462,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
         T* outz = GB + z * sB;
         T* bins = GLOBAL ? outz + c : bins_all + int64_t(wave) * K;
         const int64_t es = GLOBAL ? N : 1;
-        if (c < N) {
-            if constexpr (GLOBAL) {
-                for (int64_t k = lane; k < K; k += 64) gbin_st(bins + k * es, T(0));
-                gbin_fence();
-            } else {
-                bins_zero(bins, K);
-            }
-        }
+        if (!GLOBAL && c < N) bins_zero(bins, K);
         int mode = -1;
         const int64_t cc = c0 + sq;
         const int64_t ccl = cc < N ? cc : N - 1;

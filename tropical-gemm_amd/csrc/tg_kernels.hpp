@@ -694,15 +694,15 @@ __global__ __launch_bounds__(256) void tg_fill_zero(unsigned char* __restrict__ 
 }
 
 // Zeroes `batch` runs of `len` elements, run z starting at p + z * stride
-// (element stores: any alignment, gaps between the runs untouched).
+// (element stores: any alignment, gaps between the runs untouched).  Grid:
+// x strides over a run, y over the runs.
 template <typename T>
 __global__ __launch_bounds__(256) void tg_fill_zero_runs(T* __restrict__ p, int64_t len,
                                                           int64_t batch, int64_t stride) {
-    const int64_t total = len * batch;
     const int64_t step = int64_t(gridDim.x) * 256;
-    for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += step) {
-        const int64_t z = e / len;
-        p[z * stride + (e - z * len)] = T(0);
+    for (int64_t z = blockIdx.y; z < batch; z += gridDim.y) {
+        T* run = p + z * stride;
+        for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < len; e += step) run[e] = T(0);
     }
 }
 
