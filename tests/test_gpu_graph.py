@@ -98,10 +98,12 @@ def test_forward_paths_replay_like_eager():
                 assert torch.equal(gam, am), f"{name}: argmax, replay {rep}"
 
 
-@pytest.mark.parametrize("k", [512, 9000])
+@pytest.mark.parametrize("k", [512, 9000, 40000])
 def test_backward_replays_like_eager(k):
-    """grad_A (LDS rows) and grad_B (LDS columns; K = 9000 takes the
-    zero-filled global-atomic fallback) under capture."""
+    """grad_A and grad_B under capture: bins in LDS at K = 512 and 9000
+    (grad_B: fewer than eight columns per workgroup at 9000), in the
+    gradients themselves at K = 40000 (grad_B zero-filled by a fill kernel
+    first)."""
     from tropical_gemm import _native as nat
 
     lib = nat.load()
