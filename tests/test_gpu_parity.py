@@ -1217,3 +1217,55 @@ def test_short_k_kernel_strided_batches(sr):
         out = _strided_batched(sr, items, gap_a=gap_a, gap_c=4)
         for (x, y), (c, am) in zip(items, out):
             assert_exact(c, am, *oracle.gemm(sr, x, y))
+
+
+# Batches of more than 65535 products: the launches that put the batch on the
+# grid's third dimension split it into chunks of 65535 items (the persistent
+# K-resident kernels walk it instead).  Items on both sides of the first
+# chunk boundary, and the first and last, must equal the oracle.
+BIG_BATCH_CASES = [
+    ("maxplus", np.float32, 4, 4, 40, True, "tiles_exact"),
+    ("minplus", np.float32, 4, 4, 40, False, "shortk"),
+    ("maxmul", np.float32, 3, 5, 7, False, "tiles"),
+    ("maxplus", np.float32, 8, 8, 300, True, "dl_4x4_cl8"),
+    ("maxplus", np.float32, 16, 12, 64, False, "dl_8x8_cl32"),
+    ("minplus", np.int64, 8, 8, 300, True, "tiles_exact"),
+    ("maxplus", np.float32, 64, 64, 64, True, "kres"),
+]
+
+
+@pytest.mark.parametrize("sr,dtype,m,n,k,with_argmax,path", BIG_BATCH_CASES,
+                         ids=[f"{c[6]}-{c[0]}-{np.dtype(c[1]).name}" for c in BIG_BATCH_CASES])
+def test_batch_beyond_one_grid_dimension(sr, dtype, m, n, k, with_argmax, path):
+    from tropical_gemm import _native as nat
+
+    lib = nat.load()
+    batch = 65537
+    dt = DT_NAME[np.dtype(dtype)]
+    plan = nat.gemm_plan(sr, dt, m, n, k, with_argmax=with_argmax, batch=batch)
+    print(f"[case] batch {batch} {sr} {dt} {m}x{n}x{k} argmax={with_argmax}: {plan}", flush=True)
+    assert plan == path, plan
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(m * 1000 + k)
+    tdt = TORCH_DT[np.dtype(dtype)]
+    if np.dtype(dtype).kind == "f":
+        ta = torch.randn(batch * m * k, generator=gen, device=DEV, dtype=tdt)
+        tb = torch.randn(batch * k * n, generator=gen, device=DEV, dtype=tdt)
+    else:
+        ta = torch.randint(-1000, 1000, (batch * m * k,), generator=gen, device=DEV, dtype=tdt)
+        tb = torch.randint(-1000, 1000, (batch * k * n,), generator=gen, device=DEV, dtype=tdt)
+    c = torch.empty(batch * m * n, dtype=tdt, device=DEV)
+    am = torch.empty(batch * m * n, dtype=torch.int32, device=DEV) if with_argmax else None
+    nat.check(lib.tg_gemm_strided_batched(0, nat.SEMIRING[sr], nat.DTYPE[dt], 0, _p(ta), _p(tb), _p(c),
+                                          _p(am), batch, m, n, k, m * k, k * n, m * n, None))
+    torch.cuda.synchronize()
+    for t in (0, 1, 65534, 65535, 65536):
+        at = ta[t * m * k:(t + 1) * m * k].cpu().numpy().reshape(m, k)
+        bt = tb[t * k * n:(t + 1) * k * n].cpu().numpy().reshape(k, n)
+        ct = c[t * m * n:(t + 1) * m * n].cpu().numpy().reshape(m, n)
+        c_ref, am_ref = oracle.gemm(sr, at, bt, with_argmax=with_argmax)
+        if with_argmax:
+            amt = am[t * m * n:(t + 1) * m * n].cpu().numpy().reshape(m, n)
+            assert_exact(ct, amt, c_ref, am_ref)
+        else:
+            np.testing.assert_array_equal(ct, c_ref)
