@@ -376,7 +376,8 @@ def test_backward_bins_in_global_memory(dtype, k):
     plan_b = nat.load().tg_backward_plan(dt, 0, 0, 1, m, n, k).decode()
     print(f"[case] global bins {np.dtype(dtype).name} k={k}: {plan_a} / {plan_b}", flush=True)
     if k * np.dtype(dtype).itemsize > 128 * 1024:
-        assert "global" in plan_a and "global" in plan_b
+        # grad_B: global bins, or eight columns in passes over the keys.
+        assert "global" in plan_a and ("global" in plan_b or "passes=" in plan_b)
     rng = np.random.default_rng(k)
     g = rng.standard_normal((m, n)).astype(dtype)
     am = rng.integers(0, k, size=(m, n)).astype(np.int32)
@@ -396,7 +397,7 @@ def test_backward_b_global_bins_batched(dtype, gap):
     from tropical_gemm import _native as nat
 
     lib = nat.load()
-    batch, m, n, k = 3, 7, 130, 40000
+    batch, m, n, k = 3, 7, 130, 70000
     dt = 0 if dtype == np.float32 else 1
     plan = lib.tg_backward_plan(dt, 0, 0, batch, m, n, k).decode()
     print(f"[case] grad_B global bins batched {np.dtype(dtype).name} gap={gap}: {plan}", flush=True)
@@ -421,28 +422,43 @@ def test_backward_b_global_bins_batched(dtype, gap):
         assert (got[t * s_b + k * n:(t + 1) * s_b] == 7.0).all()
 
 
-@pytest.mark.parametrize("mult", [False, True])
-@pytest.mark.parametrize("dtype,k,waves", [(np.float32, 8192, 4), (np.float32, 12000, 3),
-                                           (np.float32, 16384, 2), (np.float32, 32768, 1),
-                                           (np.float64, 4096, 4), (np.float64, 16384, 1)])
-def test_backward_cols_long_columns_in_lds(dtype, k, waves, mult):
-    """grad_B with long columns whose bins still fit the LDS, fewer than eight
-    per workgroup: a column group that ends past N, rows that end inside a
-    tile, bins repeated within blocks, out-of-range indices, and the
-    column-by-column write-out must still give the reference's bits."""
+# grad_B with columns too long for eight columns' bins in the LDS: few rows
+# take the keys in passes over eight columns (the planner's pass length is
+# what the LDS holds: 4288 keys f32, 1872 f64), many rows fewer columns per
+# workgroup in one pass.  Cases: dtype, K, M, a fragment of the plan, MaxMul.
+LONG_COLUMNS = [
+    (np.float32, 8192, 300, "passes=2", False), (np.float32, 8192, 300, "passes=2", True),
+    (np.float32, 32768, 300, "passes=8", True), (np.float32, 40000, 60, "passes=10", False),
+    (np.float64, 16384, 300, "passes=9", True),
+    (np.float32, 8192, 4500, "waves=4 ", False), (np.float32, 12000, 4500, "waves=3 ", False),
+    (np.float32, 16384, 4500, "waves=2 ", False), (np.float32, 32768, 4500, "waves=1 ", False),
+    (np.float64, 4096, 4500, "waves=4 ", False), (np.float64, 16384, 4500, "waves=1 ", False),
+]
+
+
+@pytest.mark.parametrize("dtype,k,m,frag,mult", LONG_COLUMNS,
+                         ids=[f"{np.dtype(c[0]).name}-k{c[1]}-m{c[2]}-{c[3].strip()}{'-maxmul' if c[4] else ''}"
+                              for c in LONG_COLUMNS])
+def test_backward_cols_long_columns_in_lds(dtype, k, m, frag, mult):
+    """grad_B with long columns whose bins live in the LDS: keys on the
+    edges of the passes, a column group that ends past N, rows that end
+    inside a tile, bins repeated within blocks and out-of-range indices must
+    still give the reference's bits."""
     from tropical_gemm import _native as nat, ops
 
-    m, n = 300, 21
+    n = 21
     dt = 0 if dtype == np.float32 else 1
     plan = nat.load().tg_backward_plan(dt, 0, 0, 1, m, n, k).decode()
-    print(f"[case] grad_B long columns {np.dtype(dtype).name} k={k} mult={mult}: {plan}", flush=True)
-    assert plan.startswith("cols lds") and f"waves={waves} " in plan, plan
-    rng = np.random.default_rng(k + waves)
+    print(f"[case] grad_B long columns {np.dtype(dtype).name} m={m} k={k} mult={mult}: {plan}", flush=True)
+    assert plan.startswith("cols lds") and frag in plan, plan
+    kp = 4288 if dtype == np.float32 else 1872
+    edges = [e for p_ in range(1, 12) for e in (p_ * kp - 1, p_ * kp) if e < k] + [0, 1, k - 2, k - 1]
+    rng = np.random.default_rng(k + m)
     g = rng.standard_normal((m, n)).astype(dtype)
     am = rng.integers(0, k, size=(m, n))
-    am[:96] = rng.choice([0, 1, k // 2, k - 2, k - 1], size=(96, n))  # few bins, repeated within blocks
-    am[200:264, ::3] = k // 3  # one bin for a whole block
-    am[5, 2], am[70, 4], am[299, 20] = -1, k, k + 5  # skipped
+    am[:min(m, 96)] = rng.choice(edges, size=(min(m, 96), n))  # pass edges, repeated within blocks
+    am[200:264, ::3] = k // 3  # one bin for a whole block (where the rows exist)
+    am[5, 2], am[m - 1, 4], am[m - 1, n - 1] = -1, k, k + 5  # skipped
     a = rng.standard_normal((m, k)).astype(dtype) if mult else None
     tg_, tam = torch.from_numpy(g).to(DEV), torch.from_numpy(am.astype(np.int32)).to(DEV)
     ta = torch.from_numpy(a).to(DEV) if mult else None

@@ -101,9 +101,8 @@ def test_forward_paths_replay_like_eager():
 @pytest.mark.parametrize("k", [512, 9000, 40000])
 def test_backward_replays_like_eager(k):
     """grad_A and grad_B under capture: bins in LDS at K = 512 and 9000
-    (grad_B: fewer than eight columns per workgroup at 9000), in the
-    gradients themselves at K = 40000 (grad_B zero-filled by a fill kernel
-    first)."""
+    (grad_B in three passes over its keys at 9000), in the gradients
+    themselves at K = 40000 (grad_A; grad_B takes ten passes)."""
     from tropical_gemm import _native as nat
 
     lib = nat.load()

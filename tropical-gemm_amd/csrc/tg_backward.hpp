@@ -416,7 +416,12 @@ __global__ __launch_bounds__(256) void tg_bwd_rows(const T* __restrict__ G,
 // GLOBAL: the bins are the grad_B column itself, which the host zero-fills
 // before the launch (one coalesced pass: zeroing a column here would take
 // K stores of 4 or 8 bytes, N elements apart).
-// LDS: a stage of kStageElems per wave, W * K bins (not with GLOBAL), then
+// KP: keys per pass.  Long columns (K >> M) whose bins do not fit the LDS
+// eight at a time take their keys in passes of KP (a multiple of 4), which
+// keeps 8 columns per group, so rows leave in 8-column pieces; each pass
+// reads the group's M rows again.  Every bin still has one owner that adds
+// in row order.  KP = K with GLOBAL.
+// LDS: a stage of kStageElems per wave, W * KP bins (not with GLOBAL), then
 // the tile, kBwdTileRows (W + 1) (4 + sizeof(T)) bytes.
 // grid: any size (grid-stride over column groups), block = 64 * W, W <= 8.
 // ---------------------------------------------------------------------------
@@ -427,7 +432,8 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
                                                    const int32_t* __restrict__ IDX,
                                                    const T* __restrict__ OTHER, T* GB, int64_t M,
                                                    int64_t N, int64_t K, int64_t sC, int64_t sO,
-                                                   int64_t sB, int64_t groups_n, int64_t groups) {
+                                                   int64_t sB, int64_t groups_n, int64_t groups,
+                                                   int64_t KP) {
     extern __shared__ __align__(16) unsigned char bwd_lds[];
     constexpr int TB = kBwdTileRows / 64;  // blocks of 64 rows per tile
     const int tid = threadIdx.x;
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
     uint32_t* const cnt = reinterpret_cast<uint32_t*>(stage);
     unsigned char* const after_stage = bwd_lds + size_t(W) * kStageElems * sizeof(T);
     T* bins_all = reinterpret_cast<T*>(after_stage);
-    const int64_t bins_bytes = GLOBAL ? 0 : int64_t(W) * K * int64_t(sizeof(T));
+    const int64_t bins_bytes = GLOBAL ? 0 : int64_t(W) * KP * int64_t(sizeof(T));
     T* tile_g = reinterpret_cast<T*>(after_stage + bins_bytes);
     int32_t* tile_k =
         reinterpret_cast<int32_t*>(after_stage + bins_bytes + kBwdTileRows * stride * sizeof(T));
@@ -460,108 +466,117 @@ __global__ __launch_bounds__(512) void tg_bwd_cols(const T* __restrict__ G,
         const int32_t* kz = IDX + z * sC;
         const T* other = MULT ? OTHER + z * sO : nullptr;
         T* outz = GB + z * sB;
-        T* bins = GLOBAL ? outz + c : bins_all + int64_t(wave) * K;
-        const int64_t es = GLOBAL ? N : 1;
-        if (!GLOBAL && c < N) bins_zero(bins, K);
-        int mode = -1;
-        const int64_t cc = c0 + sq;
-        const int64_t ccl = cc < N ? cc : N - 1;
-        int32_t kr[TB];
-        T gr[TB];
-        auto stage_load = [&](int64_t i0) {
+        // Keys in passes of KP (one pass when the W columns' bins fit the LDS):
+        // each pass restages the group's rows and applies the keys of
+        // [lo, hi) to bins lo.. of this wave's column.
+        for (int64_t lo = 0; lo < K; lo += KP) {
+            const int64_t hi = K - lo < KP ? K : lo + KP;
+            // Bin of key k: bins[(k - lo) * es].
+            T* bins = GLOBAL ? outz + c : bins_all + int64_t(wave) * KP;
+            const int64_t es = GLOBAL ? N : 1;
+            if (!GLOBAL && c < N) bins_zero(bins, hi - lo);
+            int mode = -1;
+            const int64_t cc = c0 + sq;
+            const int64_t ccl = cc < N ? cc : N - 1;
+            int32_t kr[TB];
+            T gr[TB];
+            auto stage_load = [&](int64_t i0) {
 #pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                const int64_t i = i0 + 64 * t + sr;
-                const int64_t il = i < M ? i : M - 1;
-                const bool ok = i < M && cc < N;
-                const int32_t kl = kz[il * N + ccl];
-                const T gl = gz[il * N + ccl];
-                kr[t] = ok ? kl : -1;
-                gr[t] = ok ? gl : T(0);
-            }
-        };
-        stage_load(0);
-        for (int64_t i0 = 0; i0 < M; i0 += kBwdTileRows) {
-            __syncthreads();  // the previous tile's readers are done
+                for (int t = 0; t < TB; ++t) {
+                    const int64_t i = i0 + 64 * t + sr;
+                    const int64_t il = i < M ? i : M - 1;
+                    const bool ok = i < M && cc < N;
+                    const int32_t kl = kz[il * N + ccl];
+                    const T gl = gz[il * N + ccl];
+                    kr[t] = ok ? kl : -1;
+                    gr[t] = ok ? gl : T(0);
+                }
+            };
+            stage_load(0);
+            for (int64_t i0 = 0; i0 < M; i0 += kBwdTileRows) {
+                __syncthreads();  // the previous tile's readers are done
 #pragma unroll
-            for (int t = 0; t < TB; ++t) {
-                tile_k[(64 * t + sr) * stride + sq] = kr[t];
-                tile_g[(64 * t + sr) * stride + sq] = gr[t];
-            }
-            __syncthreads();
-            stage_load(i0 + kBwdTileRows);
-            if (c < N) {
-                // This column's blocks of the tile, in row order.
-                auto block = [&](int t, int32_t& key, T& g, bool& active) __attribute__((always_inline)) {
-                    const int64_t it = i0 + 64 * t;
-                    key = tile_k[(64 * t + lane) * stride + wave];
-                    g = tile_g[(64 * t + lane) * stride + wave];
-                    active = it < M && key >= 0 && int64_t(key) < K;
-                    if (MULT && active) g = g * other[(it + lane) * K + key];
-                };
-                if constexpr (GLOBAL) {
-#pragma unroll
-                    for (int t = 0; t < TB; ++t) {
-                        if (i0 + 64 * t >= M) break;
-                        int32_t key; T g; bool active;
-                        block(t, key, g, active);
-                        global_apply<T>(bins, stage, es, key, g, active, nbits);
-                    }
-                } else {
-                    int t0 = 0;
-                    if (mode < 0) {
-                        int32_t key; T g; bool active;
-                        block(0, key, g, active);
-                        mode = lds_apply<0, kCountSlots, T>(bins, cnt, key, g, active);
-                        t0 = 1;
-                    }
-                    auto blocks = [&](auto mc) __attribute__((always_inline)) {
-                        constexpr int MODE = decltype(mc)::value;
+                for (int t = 0; t < TB; ++t) {
+                    tile_k[(64 * t + sr) * stride + sq] = kr[t];
+                    tile_g[(64 * t + sr) * stride + sq] = gr[t];
+                }
+                __syncthreads();
+                stage_load(i0 + kBwdTileRows);
+                if (c < N) {
+                    // This column's blocks of the tile, in row order.
+                    auto block = [&](int t, int32_t& key, T& g, bool& active) __attribute__((always_inline)) {
+                        const int64_t it = i0 + 64 * t;
+                        key = tile_k[(64 * t + lane) * stride + wave];
+                        g = tile_g[(64 * t + lane) * stride + wave];
+                        active = it < M && int64_t(key) >= lo && int64_t(key) < hi;
+                        if (MULT && active) g = g * other[(it + lane) * K + key];
+                        key -= int32_t(lo);
+                    };
+                    if constexpr (GLOBAL) {
 #pragma unroll
                         for (int t = 0; t < TB; ++t) {
                             if (i0 + 64 * t >= M) break;
-                            if (t >= t0) {
-                                int32_t key; T g; bool active;
-                                block(t, key, g, active);
-                                lds_apply<MODE, kCountSlots, T>(bins, cnt, key, g, active);
-                            }
+                            int32_t key; T g; bool active;
+                            block(t, key, g, active);
+                            global_apply<T>(bins, stage, es, key, g, active, nbits);
                         }
-                    };
-                    if (mode == 0)
-                        blocks(std::integral_constant<int, 0>{});
-                    else if (mode == 2)
-                        blocks(std::integral_constant<int, 2>{});
-                    else
-                        blocks(std::integral_constant<int, 1>{});
-                }
-            }
-        }
-        if constexpr (!GLOBAL) {
-            __syncthreads();  // every wave's bins are complete
-            // The W columns leave together: row k of the group is W
-            // consecutive elements of grad_B.  A whole group of 8 columns
-            // whose rows start 16-byte aligned leaves in 16-byte stores, 8 / E
-            // threads per row, each gathering E columns from their bins;
-            // otherwise blockDim = 64 W, and thread tid writes column
-            // q = tid % W of rows tid / W, + 64, + 128, ...
-            constexpr int E = 16 / sizeof(T);
-            typedef T V __attribute__((ext_vector_type(E)));
-            const bool vec = W == 8 && c0 + W <= N && N % E == 0 &&
-                             (reinterpret_cast<uintptr_t>(outz) & 15) == 0;
-            if (vec) {
-                constexpr int TPR = 8 / E;
-                const int q0 = (tid % TPR) * E;
-                for (int64_t k = tid / TPR; k < K; k += 512 / TPR) {
-                    V v;
+                    } else {
+                        int t0 = 0;
+                        if (mode < 0) {
+                            int32_t key; T g; bool active;
+                            block(0, key, g, active);
+                            mode = lds_apply<0, kCountSlots, T>(bins, cnt, key, g, active);
+                            t0 = 1;
+                        }
+                        auto blocks = [&](auto mc) __attribute__((always_inline)) {
+                            constexpr int MODE = decltype(mc)::value;
 #pragma unroll
-                    for (int e = 0; e < E; ++e) v[e] = bins_all[int64_t(q0 + e) * K + k];
-                    *reinterpret_cast<V*>(outz + k * N + c0 + q0) = v;
+                            for (int t = 0; t < TB; ++t) {
+                                if (i0 + 64 * t >= M) break;
+                                if (t >= t0) {
+                                    int32_t key; T g; bool active;
+                                    block(t, key, g, active);
+                                    lds_apply<MODE, kCountSlots, T>(bins, cnt, key, g, active);
+                                }
+                            }
+                        };
+                        if (mode == 0)
+                            blocks(std::integral_constant<int, 0>{});
+                        else if (mode == 2)
+                            blocks(std::integral_constant<int, 2>{});
+                        else
+                            blocks(std::integral_constant<int, 1>{});
+                    }
                 }
-            } else if (c0 + sq < N) {
-                const T* src = bins_all + int64_t(sq) * K;
-                T* dst = outz + c0 + sq;
-                for (int64_t k = sr; k < K; k += 64) dst[k * N] = src[k];
             }
+            if constexpr (!GLOBAL) {
+                __syncthreads();  // every wave's bins are complete
+                // The W columns leave together: row k of the group is W
+                // consecutive elements of grad_B.  A whole group of 8 columns
+                // whose rows start 16-byte aligned leaves in 16-byte stores, 8 / E
+                // threads per row, each gathering E columns from their bins;
+                // otherwise blockDim = 64 W, and thread tid writes column
+                // q = tid % W of rows tid / W, + 64, + 128, ...
+                constexpr int E = 16 / sizeof(T);
+                typedef T V __attribute__((ext_vector_type(E)));
+                const bool vec = W == 8 && c0 + W <= N && N % E == 0 &&
+                                 (reinterpret_cast<uintptr_t>(outz) & 15) == 0;
+                if (vec) {
+                    constexpr int TPR = 8 / E;
+                    const int q0 = (tid % TPR) * E;
+                    for (int64_t k = lo + tid / TPR; k < hi; k += 512 / TPR) {
+                        V v;
+#pragma unroll
+                        for (int e = 0; e < E; ++e) v[e] = bins_all[int64_t(q0 + e) * KP + (k - lo)];
+                        *reinterpret_cast<V*>(outz + k * N + c0 + q0) = v;
+                    }
+                } else if (c0 + sq < N) {
+                    const T* src = bins_all + int64_t(sq) * KP;
+                    T* dst = outz + c0 + sq;
+                    for (int64_t k = lo + sr; k < hi; k += 64) dst[k * N] = src[k - lo];
+                }
+            }
+            if (lo + KP < K) __syncthreads();  // the next pass zeroes the bins and restages
         }
         __syncthreads();  // the next group zeroes the bins and restages
     }

@@ -1224,6 +1224,15 @@ size_t scratch_need(tg_dtype dt, const Problem& p, const Plan& pl) {
 constexpr int64_t kBwdMaxGrid = 16384;
 constexpr size_t kBwdLdsBudget = 128 * 1024;  // bins of one grad_A row at most
 constexpr size_t kBwdLdsLimit = 160 * 1024;   // the CU's LDS
+// grad_B takes its keys in passes (8 columns per group) when the columns'
+// bins do not fit eight at a time, a pass re-reads no more bytes than it
+// writes (the group's M rows of index and dC against its keys' gradients)
+// and there are at most kBwdMaxPasses of them.  Measured (bit-identical,
+// f32 unless noted): 1024 x 4096 x 32768 770 -> 220 us, x 16384 227 -> 107,
+// f64 1024 x 4096 x 16384 550 -> 206; 4096 x 1024 x 16384 (re-reads twice
+// the writes) 93 -> 129 and 62 passes at K = 262144 1.05 -> 1.39 ms, hence
+// the two limits.
+constexpr int64_t kBwdMaxPasses = 16;
 
 struct BwdGeometry {
     bool global = false;  // bins in the gradient itself (K too large for LDS)
@@ -1232,6 +1241,7 @@ struct BwdGeometry {
     int64_t grid = 0;     // workgroups
     int64_t groups_n = 0; // grad_B: column groups per batch item
     int64_t groups = 0;   // grad_B: column groups in total
+    int64_t kp = 0;       // grad_B: keys per pass (K: one pass)
 };
 
 // grad_A: one wave per row; a wave's LDS is its row's K bins plus its stage
@@ -1257,24 +1267,40 @@ BwdGeometry bwd_rows_geometry(int64_t rows, int64_t K, size_t es) {
 
 // grad_B: one wave per column, W <= 8 adjacent columns per workgroup: the
 // most whose bins, the staged tiles of argmax and dC (tg::kBwdTileRows x W)
-// and the waves' stages fit the CU's 160 KB (8 at K = 4096 f32: 154 KB);
+// and the waves' stages fit the CU's 160 KB (8 at K = 4096 f32: 154 KB).
+// Longer columns over few rows keep 8 columns and take their keys in passes
+// (kp: keys per pass, see kBwdMaxPasses); otherwise fewer columns, and
 // global bins when not even one column's fit.
-BwdGeometry bwd_cols_geometry(int64_t batch, int64_t N, int64_t K, size_t es) {
+BwdGeometry bwd_cols_geometry(int64_t batch, int64_t M, int64_t N, int64_t K, size_t es) {
     BwdGeometry g;
-    const size_t col_bytes = size_t(K) * es;
-    auto lds_for = [&](int64_t w, bool global) {
-        return (global ? 0 : size_t(w) * col_bytes) +
+    auto lds_for = [&](int64_t w, int64_t kp, bool global) {
+        return (global ? 0 : size_t(w) * size_t(kp) * es) +
                size_t(tg::kBwdTileRows) * size_t(w + 1) * (4 + es) +
                size_t(w) * size_t(tg::kStageElems) * es;
     };
-    int64_t w = col_bytes > kBwdLdsBudget ? 0 : 8;
-    while (w >= 1 && lds_for(w, false) > kBwdLdsLimit) --w;
-    if (w < 1) {
-        g.global = true;
-        w = 8;
+    g.kp = K;
+    // Keys per pass with 8 columns: what the LDS holds, a multiple of 4.
+    const size_t fixed8 = lds_for(8, 0, false);
+    const int64_t kp8 = int64_t((kBwdLdsLimit - fixed8) / (8 * es)) & ~int64_t(3);
+    const bool one_pass = lds_for(8, K, false) <= kBwdLdsLimit;
+    const int64_t passes = kp8 > 0 ? (K + kp8 - 1) / kp8 : 0;
+    if (!one_pass && kp8 > 0 && M * int64_t(4 + es) <= kp8 * int64_t(es) &&
+        passes <= kBwdMaxPasses) {
+        // Long columns, few rows: 8 columns in passes over the keys.
+        g.kp = kp8;
+        g.waves = 8;
+        g.lds = lds_for(8, kp8, false);
+    } else {
+        int64_t w = size_t(K) * es > kBwdLdsBudget ? 0 : 8;
+        while (w >= 1 && lds_for(w, K, false) > kBwdLdsLimit) --w;
+        if (w < 1) {
+            g.global = true;
+            w = 8;
+        }
+        g.waves = int(w);
+        g.lds = lds_for(w, K, g.global);
     }
-    g.waves = int(w);
-    g.lds = lds_for(w, g.global);
+    const int64_t w = g.waves;
     g.groups_n = (N + w - 1) / w;
     g.groups = batch * g.groups_n;
     g.grid = g.groups < kBwdMaxGrid ? g.groups : kBwdMaxGrid;
@@ -1342,7 +1368,7 @@ template <typename T, bool MULT>
 int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t batch, int64_t M,
                       int64_t N, int64_t K, int64_t sC, int64_t sO, int64_t sB, hipStream_t st) {
     if (M == 0) return zero_gradient(GB, K * N, batch, sB, st);
-    const BwdGeometry g = bwd_cols_geometry(batch, N, K, sizeof(T));
+    const BwdGeometry g = bwd_cols_geometry(batch, M, N, K, sizeof(T));
     if (g.grid == 0) return TG_OK;
     if (g.global) {
         // The bins are grad_B itself, zero-filled first in one coalesced
@@ -1354,13 +1380,13 @@ int run_backward_cols(const T* G, const int32_t* I, const T* O, T* GB, int64_t b
         if (rc != TG_OK) return rc;
         hipLaunchKernelGGL((tg::tg_bwd_cols<T, MULT, true>), dim3(unsigned(g.grid)),
                            dim3(64 * g.waves), g.lds, st, G, I, O, GB, M, N, K, sC, sO, sB,
-                           g.groups_n, g.groups);
+                           g.groups_n, g.groups, g.kp);
     } else {
         int rc = allow_lds(&tg::tg_bwd_cols<T, MULT, false>, g.lds);
         if (rc != TG_OK) return rc;
         hipLaunchKernelGGL((tg::tg_bwd_cols<T, MULT, false>), dim3(unsigned(g.grid)),
                            dim3(64 * g.waves), g.lds, st, G, I, O, GB, M, N, K, sC, sO, sB,
-                           g.groups_n, g.groups);
+                           g.groups_n, g.groups, g.kp);
     }
     TG_HIP(hipGetLastError());
     return TG_OK;
@@ -1669,10 +1695,12 @@ const char* tg_backward_plan(tg_dtype dtype, tg_layout layout, int want_a, int64
     // Row-major problem after the layout mapping (see backward_impl).
     const bool rows = (layout == TG_ROW_MAJOR) == (want_a != 0);
     const int64_t M = layout == TG_ROW_MAJOR ? m : n, N = layout == TG_ROW_MAJOR ? n : m;
-    const BwdGeometry g = rows ? bwd_rows_geometry(batch * M, k, es) : bwd_cols_geometry(batch, N, k, es);
+    const BwdGeometry g = rows ? bwd_rows_geometry(batch * M, k, es)
+                               : bwd_cols_geometry(batch, M, N, k, es);
     name = std::string(rows ? "rows" : "cols") + (g.global ? " global" : " lds") +
            " waves=" + std::to_string(g.waves) + " lds=" + std::to_string(g.lds) +
            " grid=" + std::to_string(g.grid);
+    if (!rows && g.kp < k) name += " passes=" + std::to_string((k + g.kp - 1) / g.kp);
     return name.c_str();
 }
 
