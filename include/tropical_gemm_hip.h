@@ -150,8 +150,9 @@ const char* tg_gemm_plan(tg_semiring semiring, tg_dtype dtype, tg_layout layout,
  * (want_a: 1 for grad A, 0 for grad B), e.g. "rows lds waves=2 lds=32768
  * grid=2048": the kernel family (rows / cols), where the bins live (LDS, or
  * the gradient itself for very large k), waves per workgroup, dynamic LDS
- * bytes and workgroups.  Grids are capped (the kernels loop with a grid
- * stride), so no launch dimension grows with m, n or batch.  Host logic
+ * bytes and workgroups; grad B plans end in " passes=P" when long columns
+ * take their keys in P passes.  Grids are capped (the kernels loop with a
+ * grid stride), so no launch dimension grows with m, n or batch.  Host logic
  * only; diagnostic, with no counterpart in the reference. */
 const char* tg_backward_plan(tg_dtype dtype, tg_layout layout, int want_a, int64_t batch,
                              int64_t m, int64_t n, int64_t k);
