@@ -260,6 +260,16 @@ int tg_backward_b_strided_batched(int device, tg_dtype dtype, tg_layout layout,
                                   int64_t stride_c, int64_t stride_other, int64_t stride_b,
                                   void* stream);
 
+/* Dense batched transpose: dst[z][c][r] = src[z][r][c] for batch matrices
+ * of rows x cols (each dst matrix cols x rows), any dtype.  No counterpart in
+ * the reference: it is the data movement of the tropical einsum (the
+ * permutations its contraction plan leaves to a tensor library,
+ * docs/plans/2026-01-26-tropical-einsum-design.md:245-300), which moves one
+ * group of adjacent axes past another.  rows < 2^21 (the grid); src and dst
+ * must not overlap. */
+int tg_transpose(int device, tg_dtype dtype, const void* src, void* dst, int64_t batch,
+                 int64_t rows, int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,8 @@
 """Tropical einsum on the CPU: the brute-force oracle pinned against the GEMM
 oracle and closed forms, and the host-side logic of the einsum engine
 (parsing, index classes, contraction order)."""
+import math
+
 import numpy as np
 import pytest
 
@@ -120,3 +122,41 @@ def test_contraction_order():
     assert len(path) == 3
     with pytest.raises(ValueError, match="optimize"):
         E.einsum_path(ixs, list("il"), {x: 2 for x in "ijkl"}, "dp")
+
+
+def test_layout_copies_route_group_swaps_to_the_transpose(monkeypatch):
+    """The einsum's operand copies: a permutation that moves one group of
+    adjacent axes past another goes to ``ops.transpose`` as a (batched) 2-D
+    transpose, any other to torch, and either way the result equals
+    ``permute(perm).contiguous()`` (host logic, with the device transpose
+    replaced by torch's)."""
+    import itertools
+
+    torch = pytest.importorskip("torch")
+    from tropical_gemm import einsum as E, ops
+
+    calls = []
+
+    def fake_transpose(x):
+        calls.append(tuple(x.shape))
+        return x.transpose(-1, -2).contiguous()
+
+    monkeypatch.setattr(ops, "transpose", fake_transpose)
+    monkeypatch.setattr(E, "_needs_grad", lambda *ts: False)
+    n = 0
+    for shape in [(2, 3, 4), (5, 1, 3, 2), (2, 3, 4, 5), (1, 4, 1, 3), (3, 1, 1, 2, 4)]:
+        t = torch.arange(math.prod(shape), dtype=torch.float32).reshape(shape)
+        for perm in itertools.permutations(range(len(shape))):
+            got = E._layout(t, list(perm))
+            ref = t.permute(perm).contiguous()
+            assert got.is_contiguous() and got.shape == ref.shape and torch.equal(got, ref), (shape, perm)
+            n += 1
+    assert n == 198 and len(calls) == 93
+    # [j, i, k] -> [k, j, i] is one transpose of a (j i) x k matrix.
+    calls.clear()
+    E._layout(torch.zeros(32, 64, 16), [2, 0, 1])
+    assert calls == [(32 * 64, 16)]
+    # [z, a, b] -> [z, b, a]: a batch of transposes.
+    calls.clear()
+    E._layout(torch.zeros(3, 5, 7), [0, 2, 1])
+    assert calls == [(3, 5, 7)]

@@ -190,3 +190,41 @@ def test_einsum_errors():
         E.einsum("ij->i", torch.zeros((3, 4)))
     with pytest.raises(ValueError, match="appear in one only"):
         E.contract_binary(a, torch.zeros((4, 2), device=DEV), "ij", "jk", "k", with_argmax=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.int32, torch.int64])
+@pytest.mark.parametrize("shape", [(65536, 64), (64, 65536), (1000, 37), (3, 5, 7), (65537, 2, 3),
+                                   (1, 1), (4, 128, 256)])
+def test_transpose_equals_torch(dtype, shape):
+    """tg_transpose (the einsum's data movement) against torch's transpose,
+    bit for bit: 16-byte and element kernels (aligned and ragged shapes), a
+    batch beyond one grid dimension."""
+    from tropical_gemm import ops
+
+    print(f"[case] transpose {dtype} {shape}", flush=True)
+    if dtype.is_floating_point:
+        t = torch.randn(shape, dtype=dtype, device=DEV)
+    else:
+        t = torch.randint(-(1 << 30), 1 << 30, shape, dtype=dtype, device=DEV)
+    got = ops.transpose(t)
+    assert torch.equal(got, t.transpose(-1, -2).contiguous())
+
+
+def test_einsum_operand_transposes_match_torch_copies():
+    """An einsum whose operand copies are group swaps (the E1 pattern
+    jik,lkj,lm->im) gives the same bits with the library's transpose as with
+    torch's copies."""
+    from tropical_gemm import einsum as E
+
+    g = torch.Generator(device="cpu").manual_seed(5)
+    a = torch.randn(8, 64, 16, generator=g).to(DEV)
+    b = torch.randn(64, 16, 8, generator=g).to(DEV)
+    c = torch.randn(64, 32, generator=g).to(DEV)
+    got = E.einsum("jik,lkj,lm->im", a, b, c, semiring="maxplus")
+    real = E._layout
+    try:
+        E._layout = lambda t, perm: t.permute(perm).contiguous()
+        ref = E.einsum("jik,lkj,lm->im", a, b, c, semiring="maxplus")
+    finally:
+        E._layout = real
+    assert torch.equal(got.contiguous().view(torch.int32), ref.contiguous().view(torch.int32))

@@ -1774,4 +1774,38 @@ int tg_backward_b_strided_batched(int device, tg_dtype dtype, tg_layout layout,
                          k, stride_c, stride_other, stride_b, true, other != nullptr, stream);
 }
 
+int tg_transpose(int device, tg_dtype dtype, const void* src, void* dst, int64_t batch,
+                 int64_t rows, int64_t cols, void* stream) {
+    if (!valid_dtype(dtype)) return fail(TG_ERR_INVALID_ARGUMENT, "unknown dtype " + std::to_string(dtype));
+    if (batch < 0 || rows < 0 || cols < 0) return fail(TG_ERR_DIMENSION_MISMATCH, "negative dimension");
+    if (rows > 0x7fffffffLL || cols > 0x7fffffffLL)
+        return fail(TG_ERR_DIMENSION_MISMATCH, "dimension exceeds 2^31-1");
+    if ((rows + 31) / 32 > 65535) return fail(TG_ERR_DIMENSION_MISMATCH, "rows too large for the transpose grid");
+    const int64_t elems = rows * cols;
+    if (batch > 0 && elems > 0 && (src == nullptr || dst == nullptr))
+        return fail(TG_ERR_INVALID_ARGUMENT, "src or dst is NULL");
+    int rc = select_device(device);
+    if (rc != TG_OK) return rc;
+    if (batch == 0 || elems == 0) return TG_OK;
+    hipStream_t st = as_stream(stream);
+    auto run = [&](auto tag) {
+        using T = decltype(tag);
+        const T* s = static_cast<const T*>(src);
+        T* d = static_cast<T*>(dst);
+        for (int64_t z0 = 0; z0 < batch; z0 += 65535) {
+            const int64_t nb = (batch - z0 < 65535) ? batch - z0 : 65535;
+            const int r = launch_transpose<T>(s + z0 * elems, d + z0 * elems, rows, cols, elems, elems,
+                                              nb, st);
+            if (r != TG_OK) return r;
+        }
+        return int(TG_OK);
+    };
+    switch (dtype) {
+        case TG_F32: return run(float());
+        case TG_F64: return run(double());
+        case TG_I32: return run(int32_t());
+        default: return run(int64_t());
+    }
+}
+
 }  // extern "C"

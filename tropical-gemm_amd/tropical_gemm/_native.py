@@ -73,6 +73,7 @@ SIGNATURES = {
                                        _i64, _i64, _i64, _i64, _vp], _i32),
     "tg_backward_b_strided_batched": ([_i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                        _i64, _i64, _i64, _i64, _vp], _i32),
+    "tg_transpose": ([_i32, _i32, _vp, _vp, _i64, _i64, _i64, _vp], _i32),
 }
 
 

@@ -24,8 +24,11 @@ for bit; a longer chain associates as the contraction tree does.  Labels
 summed inside one operand are reduced first, as a product with a column of
 the semiring's one (0 for MaxPlus/MinPlus, 1 for MaxMul).
 
-Permutations and reshapes are torch views and copies (data movement only, the
-plan's cuTENSOR step); every (+)/(x) runs in the HIP kernels.  Inside an
+Permutations and reshapes are data movement only (the plan's cuTENSOR step):
+views where they can be, otherwise copies -- through the library's transpose
+kernel when the permutation moves one group of adjacent axes past another,
+through torch for other permutations and for tensors that need a gradient.
+Every (+)/(x) runs in the HIP kernels.  Inside an
 einsum, which operand is the GEMM's left one and the order of the contracted
 labels are chosen so that the fewest elements are copied (an operand whose
 permuted view is already contiguous costs nothing).  Gradients flow
@@ -82,6 +85,50 @@ def _prod(sizes: Iterable[int]) -> int:
     return math.prod(sizes)
 
 
+_TRANSPOSE_MAX_ROWS = (1 << 21) - 32  # tg_transpose's grid
+
+
+def _layout(t: torch.Tensor, perm: list) -> torch.Tensor:
+    """``t.permute(perm).contiguous()``.  A permutation that moves one group
+    of adjacent axes past another -- a 2-D, or batched 2-D, transpose once the
+    axes that stay together are merged -- runs through the library's
+    transpose (``tg_transpose``); any other, and a tensor that needs a
+    gradient, through torch."""
+    v = t.permute(perm)
+    if v.is_contiguous() or t.numel() == 0:
+        return v.contiguous()
+    if _needs_grad(t) or t.dtype not in ops._DT:
+        return v.contiguous()
+    if not t.is_contiguous():
+        # A permuted view of a contiguous tensor (a contraction's result):
+        # the same copy from that tensor's own layout.
+        order = sorted(range(t.dim()), key=lambda d: -t.stride(d))
+        base = t.permute(order)
+        if not base.is_contiguous():
+            return v.contiguous()
+        pos = {a: i for i, a in enumerate(order)}
+        return _layout(base, [pos[a] for a in perm])
+    keep = [a for a in perm if t.shape[a] != 1]  # size-1 axes move no data
+    order = sorted(keep)
+    rank = {a: i for i, a in enumerate(order)}
+    sizes = [t.shape[a] for a in order]  # the moved axes' sizes, in memory order
+    groups = []  # runs of consecutive axes, in the order of the permuted view
+    for a in (rank[x] for x in keep):
+        if groups and groups[-1][-1] + 1 == a:
+            groups[-1].append(a)
+        else:
+            groups.append([a])
+    g = [_prod(sizes[a] for a in grp) for grp in groups]
+    first = [grp[0] for grp in groups]
+    if len(groups) == 2 and first[0] > first[1] and g[1] <= _TRANSPOSE_MAX_ROWS:
+        out = ops.transpose(t.reshape(g[1], g[0]))  # [A, B] -> [B, A]
+    elif len(groups) == 3 and first[0] < first[2] < first[1] and g[2] <= _TRANSPOSE_MAX_ROWS:
+        out = ops.transpose(t.reshape(g[0], g[2], g[1]))  # [Z, A, B] -> [Z, B, A]
+    else:
+        return v.contiguous()
+    return out.reshape(v.shape)
+
+
 def _check_labels(name: str, t: torch.Tensor, labels: Sequence) -> None:
     if t.dim() != len(labels):
         raise ValueError(f"{name} has {t.dim()} dimensions but {len(labels)} labels {list(labels)}")
@@ -121,7 +168,7 @@ def _reduce(t: torch.Tensor, labels: list, drop: list, semiring: str):
     keep_shape = [t.shape[labels.index(x)] for x in keep]
     rows = _prod(keep_shape)
     k = _prod(t.shape[labels.index(x)] for x in drop)
-    mat = t.permute(perm).contiguous().reshape(rows, k)
+    mat = _layout(t, perm).reshape(rows, k)
     ones = torch.full((k, 1), _ONE[semiring], dtype=t.dtype, device=t.device)
     out, _ = _gemm(semiring, mat, ones, False)
     return out.reshape(keep_shape), keep
@@ -181,7 +228,11 @@ def _contract(a, b, ia, ib, iy, semiring, with_argmax, fewest_copies):
         for swap in (False, True):
             x, lx, y, ly = (b, ib, a, ia) if swap else (a, ia, b, ib)
             lft, rgt = (right, left) if swap else (left, right)
-            for order in (con, [c for c in ly if c in con]):
+            orders = []
+            for o in (con, [c for c in lx if c in con], [c for c in ly if c in con]):
+                if o not in orders:
+                    orders.append(o)
+            for order in orders:
                 cost = (_copy_cost(x, [lx.index(c) for c in batch + lft + order]) +
                         _copy_cost(y, [ly.index(c) for c in batch + order + rgt]))
                 cands.append((cost, len(cands), swap, order))
@@ -193,8 +244,8 @@ def _contract(a, b, ia, ib, iy, semiring, with_argmax, fewest_copies):
     m = _prod(size[x] for x in left)
     n = _prod(size[x] for x in right)
     k = _prod(size[x] for x in con)  # 1 when nothing is contracted (outer product)
-    am = a.permute([ia.index(x) for x in batch + left + con]).contiguous()
-    bm = b.permute([ib.index(x) for x in batch + con + right]).contiguous()
+    am = _layout(a, [ia.index(x) for x in batch + left + con])
+    bm = _layout(b, [ib.index(x) for x in batch + con + right])
     if batch:
         c, idx = _gemm(semiring, am.reshape(nb, m, k), bm.reshape(nb, k, n), with_argmax)
     else:

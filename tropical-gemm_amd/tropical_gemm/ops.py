@@ -198,3 +198,23 @@ def backward_b_batched(grad_c: torch.Tensor, argmax: torch.Tensor, k: int,
         dev.index or 0, dt, 0, _ptr(grad_c), _ptr(argmax), _ptr(a), _ptr(out), batch, m, n, k,
         m * n, m * k, k * n, _stream(dev)))
     return out
+
+
+def transpose(t: torch.Tensor) -> torch.Tensor:
+    """``t.transpose(-1, -2).contiguous()`` of a contiguous 2-D or 3-D device
+    tensor (3-D: a batch of matrices) through ``tg_transpose``; the data
+    movement of the tropical einsum.  No autograd."""
+    t = as_tensor(t)
+    if t.dtype not in _DT:
+        raise ValueError(f"Unsupported dtype {t.dtype}: expected float32, float64, int32 or int64")
+    if t.device.type != "cuda":
+        raise ValueError("tropical_gemm GPU entry points need device tensors")
+    if t.dim() not in (2, 3) or not t.is_contiguous():
+        raise ValueError("expected a contiguous 2-D or 3-D tensor")
+    batch = t.shape[0] if t.dim() == 3 else 1
+    rows, cols = t.shape[-2], t.shape[-1]
+    out = torch.empty(t.shape[:-2] + (cols, rows), dtype=t.dtype, device=t.device)
+    lib = nat.load()
+    nat.check(lib.tg_transpose(t.device.index or 0, nat.DTYPE[_DT[t.dtype]], _ptr(t), _ptr(out),
+                               batch, rows, cols, _stream(t.device)))
+    return out
